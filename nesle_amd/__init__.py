@@ -1,0 +1,24 @@
+"""nesle_amd -- MI355X-native batched NROM (mapper 0) emulator.
+
+* ``nesle_amd._cuda_core``  drop-in for the reference's ``nesle._cuda_core``
+  (``CudaBatch``, ``CudaDeviceArrayView``, ``parse_fcs_state``), built by
+  ``python -m nesle_amd.build`` over libnesle_hip.so;
+* ``nesle_amd.abi``         ctypes binding of the C ABI (include/nesle_hip.h);
+* ``nesle_amd.synthrom``    seeded synthetic NROM ROMs and controller streams.
+
+The native pieces are imported on first use, so importing the package never
+touches a GPU; using them without the built libraries raises ImportError.
+"""
+
+from __future__ import annotations
+
+__all__ = ["load_cuda_core", "synthrom", "abi"]
+
+from . import abi, synthrom  # noqa: F401
+
+
+def load_cuda_core():
+    """The drop-in module; raises ImportError when it has not been built."""
+    from . import _cuda_core  # type: ignore[attr-defined]
+
+    return _cuda_core

@@ -1,0 +1,87 @@
+"""HIP build of the package's native code for gfx950 (MI355X).
+
+Replaces the reference's nvcc build script (scripts/build_cuda_extension.py):
+
+* ``libnesle_hip.so``  -- kernels + C ABI (include/nesle_hip.h), built by hipcc
+  for ``--offload-arch=gfx950``;
+* ``_cuda_core_native*.so`` -- the pybind11 drop-in for nesle._cuda_core
+  (re-exported by nesle_amd/_cuda_core.py), host-only C++ linked against
+  libnesle_hip.so (rpath $ORIGIN).
+
+Both land in-tree next to this file.  ``python -m nesle_amd.build`` rebuilds.
+Environment: ``HIPCC`` (default: hipcc on PATH or /opt/rocm/bin/hipcc),
+``NESLE_HIP_ARCH`` (default gfx950), ``CXX`` (default g++).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libnesle_hip.so"
+HIP_SOURCES = [CSRC / "nes_kernels.hip", CSRC / "nes_host.hip"]
+SHIM_SOURCE = CSRC / "cuda_core_module.cpp"
+
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
+    # Keep the compiler from forming packed fp32 VALU ops.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    env = os.environ.get("HIPCC")
+    if env:
+        return env
+    found = shutil.which("hipcc")
+    return found or "/opt/rocm/bin/hipcc"
+
+
+def shim_path() -> Path:
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    return PKG / f"_cuda_core_native{suffix}"
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"build step failed: {' '.join(cmd[:3])} ...")
+
+
+def build_hip(arch: str | None = None) -> Path:
+    arch = arch or os.environ.get("NESLE_HIP_ARCH", "gfx950")
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([_hipcc(), f"--offload-arch={arch}", *HIP_FLAGS, "-o", str(tmp), *map(str, HIP_SOURCES)])
+    tmp.replace(LIB)
+    return LIB
+
+
+def build_shim() -> Path:
+    import pybind11
+
+    out = shim_path()
+    tmp = out.with_name(out.name + ".tmp")
+    include = [f"-I{pybind11.get_include()}", f"-I{sysconfig.get_paths()['include']}"]
+    cxx = os.environ.get("CXX", "g++")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden", *include,
+          str(SHIM_SOURCE), "-o", str(tmp), f"-L{PKG}", "-lnesle_hip", "-Wl,-rpath,$ORIGIN"])
+    tmp.replace(out)
+    return out
+
+
+def build_all() -> None:
+    build_hip()
+    build_shim()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(f"built {LIB.name} and {shim_path().name}")

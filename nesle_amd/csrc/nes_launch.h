@@ -1,0 +1,25 @@
+// nes_launch.h -- host-side launchers for the kernels in nes_kernels.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "nes_layout.h"
+
+namespace nesle {
+
+// stats_mode: 0 none, 1 per-console counters, 2 counters + opcode/PC histograms.
+hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr,
+                       bool auto_reset, int stats_mode, hipStream_t stream);
+// Masked (null = all) reset from the snapshot bank, or power-on without one.
+hipError_t launch_reset(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
+hipError_t launch_load_blob(const DeviceState& s, const std::uint8_t* blob_src, const std::uint8_t* mask,
+                            hipStream_t stream);
+hipError_t launch_save_blob(const DeviceState& s, std::uint32_t env, std::uint8_t* out, hipStream_t stream);
+hipError_t launch_ram_obs(const DeviceState& s, std::uint8_t* obs, hipStream_t stream);
+hipError_t launch_actions_i64(std::uint8_t* dst, const long long* src, std::uint32_t n, hipStream_t stream);
+hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32_t value, hipStream_t stream);
+hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
+
+}  // namespace nesle

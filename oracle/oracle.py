@@ -1,0 +1,219 @@
+"""ctypes access to the parity oracle and to the reference-core harness.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or as the timed CPU baseline.  The
+product path (nesle_amd) never imports this module.
+
+* ``Oracle`` wraps oracle/_bin/libnes_oracle.so, the clean-room C++
+  restatement of the reference CPU core (oracle/nes_oracle.cpp).
+* ``RefConsole`` wraps oracle/_ref/libnesle_ref.so, the reference's own
+  ``nesle::Console`` compiled from its sources by ``make -C oracle ref``.
+
+Both expose the same canonical 22,896-byte state blob (layout in
+oracle/nes_oracle.cpp) so that states can be compared byte for byte.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "_bin" / "libnes_oracle.so"
+REF_SO = HERE / "_ref" / "libnesle_ref.so"
+STATE_BYTES = 22896
+
+# Offsets into the canonical state blob.
+OFF = {
+    "pc": 4, "a": 6, "x": 7, "y": 8, "sp": 9, "p": 10, "nmi_pending": 11, "cycles": 12,
+    "frame": 20, "frame_dot": 28, "ctrl": 32, "mask": 33, "status": 34, "oam_addr": 35,
+    "open_bus": 36, "read_buffer": 37, "v": 38, "t": 40, "fine_x": 42, "w": 43,
+    "scroll_x": 44, "scroll_y": 45, "c1_buttons": 46, "c1_shift": 47, "c1_count": 48,
+    "strobe": 49, "c2_count": 50, "fault": 51, "pending_dma": 52, "apu_io": 56, "ram": 80,
+    "prg_ram": 2128, "oam": 10320, "palette": 10576, "nametable": 10608, "chr_ram": 14704,
+}
+SECTIONS = {
+    # name: byte ranges of the state blob hashed (concatenated) per frame by
+    # the golden fixtures.
+    "cpu": [(4, 16)],                      # pc, a, x, y, sp, p, nmi_pending, cycles
+    "ppu": [(20, 36), (56, 24)],           # PPU scalars, pads, fault, DMA, $4000-$4017
+    "ram": [(80, 2048)],
+    "mem": [(2128, 8192), (10320, 256), (10576, 32), (10608, 4096), (14704, 8192)],
+}
+
+_U8P = ctypes.POINTER(ctypes.c_uint8)
+
+
+def build(ref: bool = False) -> None:
+    """Compile the oracle (and, if asked, the reference harness) with make."""
+    cmd = ["make", "-s", "-C", str(HERE)]
+    if ref:
+        cmd.append("ref")
+    subprocess.run(cmd, check=True)
+
+
+def fnv1a(data: bytes | np.ndarray) -> int:
+    h = 0xCBF29CE484222325
+    for b in bytes(data):
+        h ^= b
+        h = (h * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def fnv1a_np(data: np.ndarray) -> int:
+    """FNV-1a 64 of a uint8 array (vectorised over rows is not possible; loop in C)."""
+    return _oracle_lib().oracle_fnv1a(data.ctypes.data_as(_U8P), data.nbytes)
+
+
+def section_hashes(state: bytes | np.ndarray) -> dict[str, int]:
+    buf = np.frombuffer(bytes(state), dtype=np.uint8)
+    return {k: fnv1a_np(np.concatenate([buf[o:o + n] for o, n in ranges]))
+            for k, ranges in SECTIONS.items()}
+
+
+def field(state: bytes | np.ndarray, name: str, size: int = 1) -> int:
+    o = OFF[name]
+    return int.from_bytes(bytes(state[o:o + size]), "little")
+
+
+_LIB = None
+_REF = None
+
+
+def _oracle_lib():
+    global _LIB
+    if _LIB is None:
+        if not ORACLE_SO.exists():
+            build()
+        lib = ctypes.CDLL(str(ORACLE_SO))
+        lib.oracle_create.restype = ctypes.c_void_p
+        lib.oracle_create.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+        lib.oracle_destroy.argtypes = [ctypes.c_void_p]
+        lib.oracle_last_error.restype = ctypes.c_char_p
+        lib.oracle_step.restype = ctypes.c_int64
+        lib.oracle_step.argtypes = [ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64,
+                                    ctypes.POINTER(ctypes.c_float), _U8P]
+        lib.oracle_set_reward.argtypes = [ctypes.c_void_p] + [ctypes.c_uint32] * 5 + [ctypes.c_float]
+        lib.oracle_save.argtypes = [ctypes.c_void_p, _U8P]
+        lib.oracle_load.argtypes = [ctypes.c_void_p, _U8P]
+        lib.oracle_fnv1a.restype = ctypes.c_uint64
+        lib.oracle_fnv1a.argtypes = [_U8P, ctypes.c_size_t]
+        lib.oracle_splitmix64.restype = ctypes.c_uint64
+        lib.oracle_splitmix64.argtypes = [ctypes.c_uint64]
+        lib.oracle_run_batch.restype = ctypes.c_double
+        lib.oracle_run_batch.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint32,
+                                         ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,
+                                         ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]
+        _LIB = lib
+    return _LIB
+
+
+def ref_available() -> bool:
+    return REF_SO.exists()
+
+
+def _ref_lib():
+    global _REF
+    if _REF is None:
+        lib = ctypes.CDLL(str(REF_SO))
+        lib.ref_create.restype = ctypes.c_void_p
+        lib.ref_create.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+        lib.ref_destroy.argtypes = [ctypes.c_void_p]
+        lib.ref_last_error.restype = ctypes.c_char_p
+        lib.ref_step.restype = ctypes.c_int64
+        lib.ref_step.argtypes = [ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64]
+        lib.ref_save.argtypes = [ctypes.c_void_p, _U8P]
+        lib.ref_run_batch.restype = ctypes.c_double
+        lib.ref_run_batch.argtypes = _oracle_lib().oracle_run_batch.argtypes
+        _REF = lib
+    return _REF
+
+
+class Oracle:
+    """One console of the clean-room CPU core."""
+
+    def __init__(self, rom: bytes) -> None:
+        self.lib = _oracle_lib()
+        self.h = self.lib.oracle_create(rom, len(rom))
+        if not self.h:
+            raise ValueError(self.lib.oracle_last_error().decode())
+
+    def __del__(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.oracle_destroy(self.h)
+            self.h = None
+
+    def set_reward(self, kind: int = 0, x_lo: int = 0x86, x_hi: int = 0x6D, done_addr: int = 0x14,
+                   clip: int = 15, time_penalty: float = 0.0) -> None:
+        self.lib.oracle_set_reward(self.h, kind, x_lo, x_hi, done_addr, clip, time_penalty)
+
+    def step(self, buttons: int, frameskip: int = 1, max_instructions: int = 200000):
+        """One env-step; returns (instructions, reward, done)."""
+        r = ctypes.c_float()
+        d = ctypes.c_uint8()
+        n = self.lib.oracle_step(self.h, buttons & 0xFF, frameskip, max_instructions,
+                                 ctypes.byref(r), ctypes.byref(d))
+        if n < 0:
+            raise RuntimeError(self.lib.oracle_last_error().decode())
+        return n, r.value, d.value
+
+    def save(self) -> np.ndarray:
+        out = np.empty(STATE_BYTES, dtype=np.uint8)
+        self.lib.oracle_save(self.h, out.ctypes.data_as(_U8P))
+        return out
+
+    def load(self, state: np.ndarray) -> None:
+        st = np.ascontiguousarray(state, dtype=np.uint8)
+        assert st.size == STATE_BYTES
+        self.lib.oracle_load(self.h, st.ctypes.data_as(_U8P))
+
+
+class RefConsole:
+    """One console of the reference's own CPU core (oracle/_ref)."""
+
+    def __init__(self, rom: bytes) -> None:
+        self.lib = _ref_lib()
+        self.h = self.lib.ref_create(rom, len(rom))
+        if not self.h:
+            raise ValueError(self.lib.ref_last_error().decode())
+
+    def __del__(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.ref_destroy(self.h)
+            self.h = None
+
+    def step(self, buttons: int, frameskip: int = 1, max_instructions: int = 200000) -> int:
+        n = self.lib.ref_step(self.h, buttons & 0xFF, frameskip, max_instructions)
+        if n < 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        return n
+
+    def save(self) -> np.ndarray:
+        out = np.empty(STATE_BYTES, dtype=np.uint8)
+        self.lib.ref_save(self.h, out.ctypes.data_as(_U8P))
+        return out
+
+
+def run_batch(rom: bytes, num_envs: int, steps: int, frameskip: int, seed: int, threads: int,
+              kind: str = "port") -> tuple[float, int, int]:
+    """Multi-threaded CPU run; returns (seconds, ram checksum, instructions)."""
+    lib = _oracle_lib() if kind == "port" else _ref_lib()
+    fn = lib.oracle_run_batch if kind == "port" else lib.ref_run_batch
+    cs = ctypes.c_uint64()
+    ins = ctypes.c_uint64()
+    secs = fn(rom, len(rom), num_envs, steps, frameskip, seed & 0xFFFFFFFFFFFFFFFF, threads,
+              ctypes.byref(cs), ctypes.byref(ins))
+    if secs < 0:
+        raise RuntimeError("CPU batch run failed")
+    return secs, cs.value, ins.value
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1

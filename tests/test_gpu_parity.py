@@ -1,0 +1,225 @@
+"""Parity of the HIP batch (called through the C ABI) with the oracle and the
+reference's golden per-frame hashes.
+
+Bar: bit-exact canonical state (22,896 bytes per console: CPU registers and
+cycle counter, PPU registers and frame position, pads, $4000-$4017, RAM, PRG
+RAM, OAM, palette, nametables), identical instruction counts, identical
+rewards (float32 built from integers, compared exactly) and done flags.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from nesle_amd import abi, synthrom
+from oracle import oracle as O
+from tests.helpers import OracleBatch, first_diff, masks_for, say
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _rom(seed: int) -> bytes:
+    return synthrom.make_rom(seed).rom
+
+
+@pytest.mark.parametrize("rom_seed", [1, 2, 3])
+def test_single_env_matches_reference_golden(rom_seed):
+    """Config 1: one console, frame-skip 1, 600 frames, seeded pad byte per frame;
+    every recorded frame's section hashes equal the reference core's."""
+    fx = json.loads((GOLDEN / f"console_rom{rom_seed}.json").read_text())
+    rom = _rom(rom_seed)
+    assert f"{O.fnv1a(rom):016x}" == fx["rom_fnv1a"]
+    say(f"[gpu] golden rom{rom_seed}: N=1 fs=1 {fx['frames']} frames")
+    b = abi.Batch(rom, 1, frameskip=1)
+    recs = {r[0]: r for r in fx["records"]}
+    cols = fx["columns"]
+    checked = 0
+    for k in range(fx["frames"]):
+        b.set_actions(synthrom.action_masks(fx["action_seed"], 1, k))
+        b.step(stats_mode=1)
+        rec = recs.get(k + 1)
+        if rec is None:
+            continue
+        state = b.save_state(0)
+        got = O.section_hashes(state)
+        assert int(b.host(abi.VIEW_INSTRUCTIONS)[0]) == rec[1], f"frame {k + 1} instruction count"
+        for name in cols[2:]:
+            assert f"{got[name]:016x}" == rec[cols.index(name)], f"frame {k + 1} section {name}"
+        checked += 1
+    assert checked == len(fx["records"])
+
+
+def test_many_envs_match_oracle_frameskip4():
+    """64 consoles, each on its own pad stream, frame-skip 4, 30 steps: full
+    state, rewards, dones and instruction counts equal the oracle's per step."""
+    rom = _rom(7)
+    n, steps, seed = 64, 30, 77
+    say(f"[gpu] many envs: N={n} fs=4 steps={steps}")
+    b = abi.Batch(rom, n, frameskip=4)
+    ob = OracleBatch(rom, list(range(n)))
+    for k in range(steps):
+        m = masks_for(seed, n, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS), ins, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS), rew, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES), don, err_msg=f"step {k}")
+        if k % 10 == 9 or k == steps - 1:
+            for e, ref in enumerate(ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    ram = b.host(abi.VIEW_RAM)
+    for e, ref in enumerate(ob.states()):
+        assert np.array_equal(ram[e], ref[O.OFF["ram"]:O.OFF["ram"] + 2048]), f"RAM view env {e}"
+
+
+@pytest.mark.parametrize("num_envs,steps", [(4096, 4), (65536, 2)])
+def test_full_size_sampled_envs(num_envs, steps):
+    """At the benchmark sizes, sampled consoles (first, last, random) equal the
+    oracle run on their own pad streams; duplicated pad streams give identical
+    consoles (determinism across lanes, waves and XCDs)."""
+    rom = _rom(11)
+    seed = 1234
+    rng = np.random.default_rng(num_envs)
+    sample = sorted({0, 1, 63, 64, num_envs - 1, *rng.integers(0, num_envs, 6).tolist()})
+    say(f"[gpu] full size: N={num_envs} fs=4 steps={steps} sample={sample}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    ob = OracleBatch(rom, sample)
+    for k in range(steps):
+        m = masks_for(seed, num_envs, k)
+        m[num_envs // 2] = m[3]  # twin of env 3
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, don = ob.step(m, 4)
+        got_ins = b.host(abi.VIEW_INSTRUCTIONS)
+        np.testing.assert_array_equal(got_ins[sample], ins)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew)
+    for e, ref in zip(sample, ob.states()):
+        got = b.save_state(e)
+        assert np.array_equal(got, ref), f"env {e}: {first_diff(got, ref)}"
+    assert np.array_equal(b.save_state(3), b.save_state(num_envs // 2))
+    frames = b.host(abi.VIEW_FRAMES)
+    assert (frames == 4).all()
+    assert (b.host(abi.VIEW_BUDGET_HITS) == 0).all()
+
+
+def _warm_snapshots(rom: bytes, warm_frames: list[int], seed: int) -> list[np.ndarray]:
+    """Capture one snapshot per entry after that many frame-skip-1 frames."""
+    n = len(warm_frames)
+    b = abi.Batch(rom, n, frameskip=1)
+    for f in range(max(warm_frames) + 1):
+        for slot, wf in enumerate(warm_frames):
+            if wf == f:
+                b.snapshot_capture(slot, slot)
+        if f == max(warm_frames):
+            break
+        b.set_actions(masks_for(seed, n, f))
+        b.step()
+    assert b.num_levels == n
+    return [b.snapshot_export(s) for s in range(n)]
+
+
+def test_snapshot_autoreset_xdelta_reward():
+    """Config 3 in miniature: 8 snapshots captured after seeded warm-up frames,
+    done byte patched so episodes end within the run, x-delta reward with time
+    penalty, fused auto-reset; rewards, dones and post-reset states equal the
+    oracle restoring the same snapshot."""
+    rom_info = synthrom.make_rom(5)
+    rom = rom_info.rom
+    warm = [100, 150, 200, 250, 300, 350, 400, 450]
+    say("[gpu] snapshot bank: warm-up capture of 8 levels")
+    snaps = _warm_snapshots(rom, warm, seed=55)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 1 + i  # done after 8*(1+i) frames at most
+    blobs = [bytes(s) for s in snaps]
+    n, steps = 64, 40
+    levels = (np.arange(n) % 8).astype(np.uint8)
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.25)
+    say(f"[gpu] snapshot auto-reset: N={n} fs=4 steps={steps}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.25)
+    b.set_snapshots(blobs, levels)
+    ob = OracleBatch(rom, list(range(n)), reward=reward)
+    for e, c in enumerate(ob.cons):
+        c.load(snaps[levels[e]])
+    for e, ref in enumerate(ob.states()):
+        assert np.array_equal(b.save_state(e), ref), f"initial env {e}"
+    total_done = 0
+    for k in range(steps):
+        m = masks_for(99, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS), rew, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES), don, err_msg=f"step {k}")
+        for e in np.nonzero(don)[0]:
+            ob.cons[e].load(snaps[levels[e]])
+        total_done += int(don.sum())
+        if k % 8 == 7:
+            for e, ref in enumerate(ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert total_done > n  # every env finished at least one episode
+    assert (np.unique(b.host(abi.VIEW_REWARDS)) <= 15 - 0.25).all()
+
+
+def test_reset_envs_and_state_roundtrip():
+    """Masked reset returns exactly the selected consoles to power-on; a saved
+    state loaded into other consoles makes them identical; int64 device
+    actions equal uint8 host actions."""
+    import torch
+
+    rom = _rom(3)
+    n = 256
+    say(f"[gpu] reset/state round trip: N={n}")
+    b = abi.Batch(rom, n, frameskip=4)
+    power_on = b.save_state(0)
+    for k in range(3):
+        b.set_actions(masks_for(5, n, k))
+        b.step()
+    mask = np.zeros(n, dtype=np.uint8)
+    mask[::3] = 1
+    before = [b.save_state(e) for e in (1, 2)]
+    b.reset_envs(mask)
+    for e in (0, 3, 255):
+        assert np.array_equal(b.save_state(e), power_on)
+    assert np.array_equal(b.save_state(1), before[0]) and np.array_equal(b.save_state(2), before[1])
+    st = b.save_state(2)
+    lm = np.zeros(n, dtype=np.uint8)
+    lm[10:20] = 1
+    b.load_state(st, lm)
+    for e in range(10, 20):
+        assert np.array_equal(b.save_state(e), st)
+    # int64 device actions vs uint8 host actions on a twin batch.
+    b2 = abi.Batch(rom, n, frameskip=4)
+    b3 = abi.Batch(rom, n, frameskip=4)
+    m = masks_for(8, n, 0)
+    b2.set_actions(torch.from_numpy(m.astype(np.int64) | 0x300).cuda())
+    b2.step()
+    b3.set_actions(m)
+    b3.step()
+    np.testing.assert_array_equal(b2.host(abi.VIEW_RAM), b3.host(abi.VIEW_RAM))
+
+
+def test_profile_counts_match_instructions():
+    """step_profile's opcode histogram sums to the per-console instruction
+    counts; only official opcodes appear."""
+    rom = _rom(4)
+    n = 128
+    say(f"[gpu] profile: N={n}")
+    b = abi.Batch(rom, n, frameskip=4)
+    b.set_actions(masks_for(1, n, 0))
+    b.step(stats_mode=2)
+    ops = b.host(abi.VIEW_OPCODES)
+    pcs = b.host(abi.VIEW_PCS)
+    ins = b.host(abi.VIEW_INSTRUCTIONS)
+    assert ops.sum() == ins.sum() == pcs.sum()
+    assert set(np.nonzero(ops)[0].tolist()) <= synthrom.OFFICIAL_OPCODES
