@@ -163,6 +163,21 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def copy_calibration(mib: int) -> int:
+    """A plain device-to-device copy of known size: each dispatch reads and
+    writes exactly ``mib`` MiB, so rocprof's per-dispatch FETCH_SIZE and
+    WRITE_SIZE for it give the counters' scale on this GPU."""
+    import torch
+
+    src = torch.ones(mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": mib << 20, "dispatches": 5}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,7 +188,11 @@ def main() -> int:
     ap.add_argument("--small-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 5 times (scales rocprof FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; the consoles shard trivially "
                                    "across GPUs but no multi-GPU figure is produced (--gpus 1)"}))

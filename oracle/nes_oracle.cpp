@@ -745,6 +745,39 @@ std::int64_t oracle_step(void* h, std::uint8_t buttons, std::uint32_t frameskip,
     }
 }
 
+// One console instruction (console.hpp:108-135): NMI entry, the instruction,
+// DMA stall, PPU dots.  Returns the CPU cycles it took (NMI and DMA included)
+// and stores the frames it completed in *frames; -1 on an illegal opcode.
+std::int64_t oracle_step_instruction(void* h, std::uint32_t* frames) {
+    auto* e = static_cast<Env*>(h);
+    try {
+        const std::uint64_t before = e->m.cycles;
+        const std::uint32_t f = e->m.step_instruction();
+        if (frames) *frames = f;
+        return static_cast<std::int64_t>(e->m.cycles - before);
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1;
+    }
+}
+
+// CPU bus accesses with their side effects (console.hpp:49-101): the
+// known-answer tests drive registers, mirrors, DMA and the pads through these.
+std::uint32_t oracle_bus_read(void* h, std::uint32_t addr) {
+    return static_cast<Env*>(h)->m.read(static_cast<std::uint16_t>(addr));
+}
+void oracle_bus_write(void* h, std::uint32_t addr, std::uint32_t value) {
+    static_cast<Env*>(h)->m.write(static_cast<std::uint16_t>(addr), static_cast<std::uint8_t>(value));
+}
+
+// PPU memory space read ($0000-$3FFF, ppu.hpp:280-338) without side effects.
+std::uint32_t oracle_ppu_peek(void* h, std::uint32_t addr) {
+    return static_cast<Env*>(h)->m.vram_read(static_cast<std::uint16_t>(addr));
+}
+
+// Advance the PPU alone by `dots` (ppu.hpp:46-76); returns frames completed.
+std::uint32_t oracle_ppu_run(void* h, std::uint32_t dots) { return static_cast<Env*>(h)->m.ppu_run(dots); }
+
 void oracle_save(void* h, std::uint8_t* out) { static_cast<Env*>(h)->m.save(out); }
 
 // Restore a full-state blob; reward baselines are re-seeded from its RAM.

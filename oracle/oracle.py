@@ -50,7 +50,7 @@ _U8P = ctypes.POINTER(ctypes.c_uint8)
 
 def build(ref: bool = False) -> None:
     """Compile the oracle (and, if asked, the reference harness) with make."""
-    cmd = ["make", "-s", "-C", str(HERE)]
+    cmd = ["make", "-s", "-C", str(HERE), "all"]
     if ref:
         cmd.append("ref")
     subprocess.run(cmd, check=True)
@@ -98,6 +98,15 @@ def _oracle_lib():
         lib.oracle_step.argtypes = [ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64,
                                     ctypes.POINTER(ctypes.c_float), _U8P]
         lib.oracle_set_reward.argtypes = [ctypes.c_void_p] + [ctypes.c_uint32] * 5 + [ctypes.c_float]
+        lib.oracle_step_instruction.restype = ctypes.c_int64
+        lib.oracle_step_instruction.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
+        lib.oracle_bus_read.restype = ctypes.c_uint32
+        lib.oracle_bus_read.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        lib.oracle_bus_write.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]
+        lib.oracle_ppu_peek.restype = ctypes.c_uint32
+        lib.oracle_ppu_peek.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        lib.oracle_ppu_run.restype = ctypes.c_uint32
+        lib.oracle_ppu_run.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
         lib.oracle_save.argtypes = [ctypes.c_void_p, _U8P]
         lib.oracle_load.argtypes = [ctypes.c_void_p, _U8P]
         lib.oracle_fnv1a.restype = ctypes.c_uint64
@@ -127,6 +136,9 @@ def _ref_lib():
         lib.ref_step.restype = ctypes.c_int64
         lib.ref_step.argtypes = [ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64]
         lib.ref_save.argtypes = [ctypes.c_void_p, _U8P]
+        lib.ref_load.argtypes = [ctypes.c_void_p, _U8P]
+        lib.ref_step_instruction.restype = ctypes.c_int64
+        lib.ref_step_instruction.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
         lib.ref_run_batch.restype = ctypes.c_double
         lib.ref_run_batch.argtypes = _oracle_lib().oracle_run_batch.argtypes
         _REF = lib
@@ -161,6 +173,26 @@ class Oracle:
             raise RuntimeError(self.lib.oracle_last_error().decode())
         return n, r.value, d.value
 
+    def step_instruction(self) -> tuple[int, int]:
+        """One console instruction; returns (CPU cycles incl. NMI/DMA, frames completed)."""
+        f = ctypes.c_uint32()
+        c = self.lib.oracle_step_instruction(self.h, ctypes.byref(f))
+        if c < 0:
+            raise RuntimeError(self.lib.oracle_last_error().decode())
+        return c, f.value
+
+    def read(self, addr: int) -> int:
+        return self.lib.oracle_bus_read(self.h, addr)
+
+    def write(self, addr: int, value: int) -> None:
+        self.lib.oracle_bus_write(self.h, addr, value)
+
+    def ppu_peek(self, addr: int) -> int:
+        return self.lib.oracle_ppu_peek(self.h, addr)
+
+    def ppu_run(self, dots: int) -> int:
+        return self.lib.oracle_ppu_run(self.h, dots)
+
     def save(self) -> np.ndarray:
         out = np.empty(STATE_BYTES, dtype=np.uint8)
         self.lib.oracle_save(self.h, out.ctypes.data_as(_U8P))
@@ -192,10 +224,22 @@ class RefConsole:
             raise RuntimeError(self.lib.ref_last_error().decode())
         return n
 
+    def step_instruction(self) -> tuple[int, int]:
+        f = ctypes.c_uint32()
+        c = self.lib.ref_step_instruction(self.h, ctypes.byref(f))
+        if c < 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        return c, f.value
+
     def save(self) -> np.ndarray:
         out = np.empty(STATE_BYTES, dtype=np.uint8)
         self.lib.ref_save(self.h, out.ctypes.data_as(_U8P))
         return out
+
+    def load(self, state: np.ndarray) -> None:
+        st = np.ascontiguousarray(state, dtype=np.uint8)
+        assert st.size == STATE_BYTES
+        self.lib.ref_load(self.h, st.ctypes.data_as(_U8P))
 
 
 def run_batch(rom: bytes, num_envs: int, steps: int, frameskip: int, seed: int, threads: int,

@@ -119,6 +119,63 @@ void ref_save(void* h, std::uint8_t* o) {
     std::memcpy(o + 14704, p.chr_ram_.data(), 8192);
 }
 
+// Inverse of ref_save: every field of the canonical blob into the Console.
+// Pad 2 has no buttons; it shares pad 1's strobe line.
+void ref_load(void* h, const std::uint8_t* s) {
+    auto* e = static_cast<RefEnv*>(h);
+    auto& c = e->console;
+    auto& p = c.ppu_;
+    auto u16 = [&](std::size_t off) { return static_cast<std::uint16_t>(s[off] | (s[off + 1] << 8)); };
+    auto u32 = [&](std::size_t off) {
+        std::uint32_t r = 0;
+        for (int i = 0; i < 4; ++i) r |= std::uint32_t(s[off + i]) << (8 * i);
+        return r;
+    };
+    auto u64 = [&](std::size_t off) {
+        std::uint64_t r = 0;
+        for (int i = 0; i < 8; ++i) r |= std::uint64_t(s[off + i]) << (8 * i);
+        return r;
+    };
+    e->cpu.pc = u16(4);
+    e->cpu.a = s[6]; e->cpu.x = s[7]; e->cpu.y = s[8]; e->cpu.sp = s[9]; e->cpu.p = s[10];
+    p.nmi_pending_ = s[11] != 0;
+    e->cpu.cycles = u64(12);
+    p.frame_ = u64(20);
+    const std::uint32_t fd = u32(28);
+    p.scanline_ = static_cast<std::int16_t>(fd / 341u);
+    p.dot_ = static_cast<std::uint16_t>(fd % 341u);
+    p.ctrl_ = s[32]; p.mask_ = s[33]; p.status_ = s[34]; p.oam_addr_ = s[35];
+    p.open_bus_ = s[36]; p.read_buffer_ = s[37];
+    p.v_ = u16(38); p.t_ = u16(40);
+    p.x_ = s[42]; p.w_ = s[43] != 0; p.scroll_x_ = s[44]; p.scroll_y_ = s[45];
+    c.controller1_.buttons_ = s[46]; c.controller1_.shift_register_ = s[47];
+    c.controller1_.shift_count_ = s[48]; c.controller1_.strobe_ = s[49] != 0;
+    c.controller2_.buttons_ = 0; c.controller2_.shift_register_ = 0;
+    c.controller2_.shift_count_ = s[50]; c.controller2_.strobe_ = s[49] != 0;
+    c.pending_dma_cycles_ = u32(52);
+    std::memcpy(c.apu_io_.data(), s + 56, 24);
+    std::memcpy(c.cpu_ram_.data(), s + 80, 2048);
+    std::memcpy(c.prg_ram_.data(), s + 2128, 8192);
+    std::memcpy(p.oam_.data(), s + 10320, 256);
+    std::memcpy(p.palette_ram_.data(), s + 10576, 32);
+    std::memcpy(p.nametable_ram_.data(), s + 10608, 4096);
+    std::memcpy(p.chr_ram_.data(), s + 14704, 8192);
+}
+
+// Console::step_cpu_instruction (console.hpp:108-135); returns CPU cycles
+// (NMI and DMA included), frames completed in *frames, -1 on an exception.
+std::int64_t ref_step_instruction(void* h, std::uint32_t* frames) {
+    auto* e = static_cast<RefEnv*>(h);
+    try {
+        const auto r = e->console.step_cpu_instruction(e->cpu);
+        if (frames) *frames = r.frames_completed;
+        return static_cast<std::int64_t>(r.cpu_cycles);
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1;
+    }
+}
+
 // Same contract as oracle_run_batch (oracle/nes_oracle.cpp), over the
 // reference Console.  Used as the "reference" CPU baseline.
 double ref_run_batch(const std::uint8_t* ines, std::size_t len, std::uint32_t n_envs,
