@@ -259,8 +259,9 @@ struct nesle_batch {
         add(&ds.scroll_y, n); add(&ds.c1_buttons, n); add(&ds.c1_shift, n); add(&ds.c1_count, n);
         add(&ds.strobe, n); add(&ds.c2_count, n);
         add(&ds.apu_io, nesle::kApuIoBytes * P);
-        add(&ds.ram, nesle::kRamBytes * P);
-        add(&ds.prg_ram, nesle::kPrgRamBytes * P);
+        // RAM rows 0-2047 and PRG RAM rows 2048-10239 form one interleaved array,
+        // so the step kernel reaches both with one row * pitch + env offset.
+        add(&ds.ram, static_cast<std::size_t>(nesle::kRamBytes + nesle::kPrgRamBytes) * P);
         add(&ds.oam, nesle::kOamBytes * P);
         add(&ds.palette, nesle::kPaletteBytes * P);
         add(&ds.nametable, static_cast<std::size_t>(ds.nt_bytes) * P);
@@ -282,6 +283,7 @@ struct nesle_batch {
             *s.dst = static_cast<std::uint8_t*>(arena) + off;
             off += s.bytes;
         }
+        ds.prg_ram = ds.ram + static_cast<std::size_t>(nesle::kRamBytes) * P;
         ds.actions = actions;
         ds.prg_rom = d_prg;
         ds.chr_rom = rom.chr.empty() ? nullptr : d_chr;

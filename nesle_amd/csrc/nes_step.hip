@@ -1,30 +1,37 @@
 // nes_step.hip -- the batched NROM console step for gfx950 (MI355X).
 //
-// One wave64 lane per console.  Per launch a lane runs `frameskip` NES frames:
-// NMI entry, the 6502 instruction, OAM DMA stall, lazy PPU settlement at the
-// timing events, then the reward/done rule and, if asked, a fused auto-reset
-// from the snapshot bank.  Semantics follow the reference's CPU core
-// (cpp/include/nesle/console.hpp:108-150, cpu.hpp:377-730, ppu.hpp:46-395);
-// the launch structure mirrors the reference's console_step_kernel
-// (cpp/src/cuda/kernels.cu:19-104) and reset kernels (kernels.cu:177-203).
+// One lane per console.  Per launch a lane runs `frameskip` NES frames: NMI
+// entry, the 6502 instruction, OAM DMA, lazy PPU settlement at the timing
+// events, then the reward/done rule and, if asked, a fused auto-reset from the
+// snapshot bank.  Semantics follow the reference's CPU core
+// (cpp/include/nesle/console.hpp:49-150, cpu.hpp:84-730, ppu.hpp:46-395,
+// controller.hpp:18-67); the launch mirrors the reference's console_step_kernel
+// (cpp/src/cuda/kernels.cu:19-104) and its snapshot reset (kernels.cu:195-203).
 //
-// MI355X-specific choices:
-//  * PRG ROM (<= 32 KB) and the 256-entry microcode table are staged into LDS
-//    once per workgroup; every opcode/operand fetch is an LDS read.
-//  * Instructions execute on one branch-free microcoded datapath
-//    (nes_layout.h): a wave's cost does not grow with the number of distinct
-//    opcodes its 64 lanes hold; only control-transfer/stack opcodes and I/O
-//    registers take divergent paths.
-//  * CPU registers and the per-instruction PPU scalars (frame_dot, status,
-//    ctrl, mask, nmi) live in VGPRs for the whole launch.
-//  * Console RAM and the other per-console arrays are address-major
-//    interleaved ([addr][env]) so lanes on the same code path coalesce.
-//  * Workgroups are remapped so that each XCD (blockIdx % 8 on MI355X) owns a
-//    contiguous range of consoles: interleaved cache lines stay in one L2.
-//  * The PPU is settled lazily: only at a timing event (sprite-0 dot, vblank,
-//    pre-render, frame end).  The sprite-0 dot is always an event, so the
-//    rendering-enable test sees the mask exactly as the reference CPU core's
-//    per-dot PPU does.
+// Cost model on MI355X (measured): one wave issues one instruction every ~4.3
+// cycles, an LDS round trip takes ~84 cycles and a global one ~250.  At 65,536
+// consoles there is exactly one wave per SIMD, so the kernel is bound by the
+// instructions a wave issues per emulated 6502 instruction and by the memory
+// round trips on that path.  Hence:
+//  * Geometry: 4 waves per workgroup, L = N/1024 (rounded up to a power of
+//    two, at most 64) consoles per wave, so every SIMD holds one wave however
+//    small the batch.  Small batches thus get few, short waves (less
+//    divergence) instead of a few full waves on a few CUs.
+//  * LDS holds the PRG ROM (32 KB), the 128-bit microcode table and console
+//    RAM: all 2 KB of it when 4L consoles fit (L <= 8), otherwise the zero page
+//    and $0180-$01FF.  Each console's RAM is one contiguous LDS block whose
+//    stride is 1 dword modulo the bank count, so lanes at equal addresses hit
+//    distinct banks.  Remaining RAM rows and PRG RAM are address-major
+//    interleaved in HBM (row * pitch + env): lanes at equal addresses coalesce.
+//  * Registers A/X/Y/SP are packed in one VGPR and read/written with bitfield
+//    extract/insert driven by the microcode (nes_micro.h).  Every PPU and pad
+//    register lives in a VGPR for the whole launch.
+//  * The datapath is branch-free; stack/control opcodes, I/O registers, NMI
+//    entry and PPU settlement take divergent side paths.
+//  * OAM DMA is done by the whole wave for one console at a time (4 bytes per
+//    lane) instead of a 256-iteration loop in one lane.
+//  * The CPU cycle counter is not updated per instruction: every cycle is 3
+//    PPU dots, so cycles advance by (dots advanced) / 3 at the end.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -32,95 +39,102 @@
 #include "nes_device.h"
 #include "nes_launch.h"
 #include "nes_layout.h"
+#include "nes_micro.h"
 
 namespace nesle {
 namespace {
 
-__constant__ std::uint64_t c_micro[256] = {
-#define NESLE_E(i) mc::kTable.e[i]
-#define NESLE_E8(i) NESLE_E(i), NESLE_E(i + 1), NESLE_E(i + 2), NESLE_E(i + 3), NESLE_E(i + 4), \
-                    NESLE_E(i + 5), NESLE_E(i + 6), NESLE_E(i + 7)
-#define NESLE_E64(i) NESLE_E8(i), NESLE_E8(i + 8), NESLE_E8(i + 16), NESLE_E8(i + 24), \
-                     NESLE_E8(i + 32), NESLE_E8(i + 40), NESLE_E8(i + 48), NESLE_E8(i + 56)
-    NESLE_E64(0), NESLE_E64(64), NESLE_E64(128), NESLE_E64(192)
-#undef NESLE_E64
-#undef NESLE_E8
-#undef NESLE_E
+__constant__ uint4 c_micro[256] = {
+#define NESLE_W(i) {mc::kTable.e[i].d[0], mc::kTable.e[i].d[1], mc::kTable.e[i].d[2], mc::kTable.e[i].d[3]}
+#define NESLE_W8(i) NESLE_W(i), NESLE_W(i + 1), NESLE_W(i + 2), NESLE_W(i + 3), NESLE_W(i + 4), NESLE_W(i + 5), \
+                    NESLE_W(i + 6), NESLE_W(i + 7)
+#define NESLE_W64(i) NESLE_W8(i), NESLE_W8(i + 8), NESLE_W8(i + 16), NESLE_W8(i + 24), NESLE_W8(i + 32), \
+                     NESLE_W8(i + 40), NESLE_W8(i + 48), NESLE_W8(i + 56)
+    NESLE_W64(0), NESLE_W64(64), NESLE_W64(128), NESLE_W64(192)
+#undef NESLE_W64
+#undef NESLE_W8
+#undef NESLE_W
 };
 
-constexpr std::uint32_t kMaxBlock = 256;
+extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 
-// Dynamic LDS layout of the step kernel (bytes):
-//   [0, 32768)            PRG ROM, a 16 KB image mirrored to fill 32 KB
-//   [32768, 32784)        padding read by the two-dword instruction fetch
-//   [32784, 34832)        microcode table (256 x 8 B)
-//   [34832, +256*T)       zero page of the block's T consoles
-//   [.., +128*T)          top of the stack page ($0180-$01FF)
-// Console bytes are dword-interleaved: byte `a` of lane t lives in dword
-// (a >> 2) * T + t at byte a & 3, so a wave's 64 lanes always touch 64
-// different banks whatever addresses they hold.
-constexpr std::uint32_t kLdsMicro = 32784;
-constexpr std::uint32_t kLdsZp = kLdsMicro + 256 * 8;
-constexpr std::uint32_t kZpBytes = 256;
-constexpr std::uint32_t kStackLo = 0x180;      // stack bytes $0180-$01FF live in LDS
-constexpr std::uint32_t kStackBytes = 128;
+constexpr std::uint32_t kBlock = 256;           // 4 waves
+constexpr std::uint32_t kLdsMicro = 32768;      // 256 x 16 B
+constexpr std::uint32_t kLdsRam = 32768 + 4096; // console RAM blocks
+constexpr std::uint32_t kSplitStride = 388;     // $0000-$00FF, $0180-$01FF, 4 spare bytes
+constexpr std::uint32_t kFullStride = 2052;     // $0000-$07FF, 4 spare bytes
+constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 
-constexpr std::uint32_t lds_bytes(std::uint32_t threads) {
-    return kLdsZp + (kZpBytes + kStackBytes) * threads;
+constexpr std::uint32_t lds_bytes(std::uint32_t consoles, bool full) {
+    return kLdsRam + consoles * (full ? kFullStride : kSplitStride);
 }
 
-// Maps the hardware block index to the logical console block so that XCD k
-// (blocks dispatched round-robin, b % 8 == k) owns one contiguous range.
+// XCD k (workgroups dispatched round-robin, b % 8 == k) owns one contiguous
+// range of consoles, so interleaved cache lines stay in one L2.
 __device__ __forceinline__ std::uint32_t xcd_block(std::uint32_t b, std::uint32_t nb) {
     const std::uint32_t q = nb >> 3, r = nb & 7, xcd = b & 7;
     return xcd * q + (xcd < r ? xcd : r) + (b >> 3);
 }
 
-struct Lane {
+__device__ __forceinline__ std::uint32_t ubfe(std::uint32_t v, std::uint32_t off, std::uint32_t w) {
+    return __builtin_amdgcn_ubfe(v, off, w);
+}
+
+// Dots from `fd` to the next timing event: sprite-0 dot, vblank, pre-render
+// line, frame end (ppu.hpp:19-25,136-147).  Signed differences keep every
+// candidate comparison a plain select.
+__device__ __forceinline__ std::uint32_t to_event(std::uint32_t fd) {
+    const std::int32_t c = static_cast<std::int32_t>(fd);
+    std::int32_t d = static_cast<std::int32_t>(kFrameDots) - c;
+    const std::int32_t s0 = static_cast<std::int32_t>(kSprite0Dot) - c;
+    const std::int32_t vb = static_cast<std::int32_t>(kVblankDot) - c;
+    const std::int32_t pr = static_cast<std::int32_t>(kPreRenderDot) - c;
+    d = (s0 > 0 && s0 < d) ? s0 : d;
+    d = (vb > 0 && vb < d) ? vb : d;
+    d = (pr > 0 && pr < d) ? pr : d;
+    return static_cast<std::uint32_t>(d);
+}
+
+template <bool kFull>
+struct Console {
+    static constexpr std::uint32_t kStride = kFull ? kFullStride : kSplitStride;
+    static constexpr std::uint32_t kSpare = kFull ? 2048u : 384u;
+
     const DeviceState& s;
-    std::uint8_t* lds;         // generic pointer to the block's dynamic LDS
-    std::uint8_t* ram_lane;    // s.ram + env (generic pointer into HBM)
-    std::uint32_t env;
-    std::uint32_t pitch;
-    std::uint32_t row;         // 4 * threads per block: one dword row of LDS
-    std::uint32_t lane4;       // 4 * thread index
-    std::uint32_t stk_base;    // LDS offset of the stack rows
+    std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
-    // CPU registers.
-    std::uint32_t pc, a, x, y, sp, p;
-    std::uint64_t cycles;
-    // Per-instruction PPU scalars.
+    // CPU.
+    std::uint32_t pc, regs, p;
+    // PPU.
     std::uint32_t frame_dot, status, ctrl, mask, nmi;
-    std::uint32_t frames;      // frames completed in this launch
-    std::uint32_t dma;         // DMA stall cycles owed by the current instruction
+    std::uint32_t oam_addr, open_bus, read_buffer, v, t, fine_x, w, scroll_x, scroll_y;
+    // Pads.
+    std::uint32_t c1_buttons, c1_shift, c1_count, strobe, c2_count;
+    // OAM DMA requested by the current instruction (page | 0x100).
+    std::uint32_t dma;
     std::uint32_t fault;
 
-    __device__ __forceinline__ std::uint8_t* cell(std::uint8_t* base, std::uint32_t addr) const {
-        return base + (static_cast<std::size_t>(addr) * pitch + env);
+    // ---- console RAM ($0000-$07FF, mirrored to $1FFF) -------------------------
+    __device__ __forceinline__ static bool ram_in_lds(std::uint32_t ra) {
+        return kFull || ((0xBu >> (ra >> 7)) & 1u);  // rows $000-$0FF and $180-$1FF
+    }
+    __device__ __forceinline__ static std::uint32_t ram_lds_off(std::uint32_t ra) {
+        return kFull ? ra : ra - ((ra >> 1) & 0x80u);
+    }
+    __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return row * pitch + env; }
+    __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t ra) const {
+        if (ram_in_lds(ra)) return lds[base + ram_lds_off(ra)];
+        return s.ram[goff(ra)];
+    }
+    __device__ __forceinline__ void ram_wr(std::uint32_t ra, std::uint32_t val) const {
+        if (ram_in_lds(ra)) {
+            lds[base + ram_lds_off(ra)] = static_cast<std::uint8_t>(val);
+        } else {
+            s.ram[goff(ra)] = static_cast<std::uint8_t>(val);
+        }
     }
 
-    // Generic pointer for a CPU address in RAM ($0000-$1FFF) or PRG ROM
-    // ($8000-$FFFF): PRG, zero page and the stack top resolve to LDS, the
-    // rest of RAM to HBM.  One FLAT access then serves every lane.
-    __device__ __forceinline__ std::uint8_t* gptr(std::uint32_t addr) const {
-        const std::uint32_t ra = addr & 0x7FF;
-        const bool rom = addr >= 0x8000;
-        const bool zp = ra < kZpBytes;
-        const bool stk = (ra >> 7) == (kStackLo >> 7);
-        const std::uint32_t sub = zp ? ra : (ra & 0x7F);
-        const std::uint32_t rowoff = (sub >> 2) * row + lane4 + (sub & 3);
-        const std::uint32_t loff = rom ? (addr & 0x7FFF) : (zp ? kLdsZp : stk_base) + rowoff;
-        std::uint8_t* lp = lds + loff;
-        std::uint8_t* gp = ram_lane + static_cast<std::size_t>(ra) * pitch;
-        return (rom || zp || stk) ? lp : gp;
-    }
-
-    // ---- console RAM ($0000-$1FFF) -------------------------------------------
-    __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t addr) const { return *gptr(addr & 0x7FF); }
-    __device__ __forceinline__ void ram_wr(std::uint32_t addr, std::uint32_t v) const {
-        *gptr(addr & 0x7FF) = static_cast<std::uint8_t>(v);
-    }
-    // ---- PPU memory (ppu.hpp:280-338) ----------------------------------------
+    // ---- PPU memory (ppu.hpp:280-338) -------------------------------------------
     __device__ std::uint32_t nt_index(std::uint32_t addr) const {
         const std::uint32_t i = (addr - 0x2000) & 0x0FFF;
         if (s.nt_mode == 2) return i;
@@ -128,392 +142,172 @@ struct Lane {
         return (i & 0x03FF) | ((i & 0x0800) >> 1);
     }
     __device__ static std::uint32_t pal_index(std::uint32_t addr) {
-        std::uint32_t i = addr & 0x1F;
+        const std::uint32_t i = addr & 0x1F;
         return ((i & 0x13) == 0x10) ? (i & 0x0F) : i;
     }
     __device__ std::uint32_t vram_rd(std::uint32_t addr) const {
         addr &= 0x3FFF;
         if (addr < 0x2000) {
             if (s.chr_size != 0) return s.chr_rom[addr % s.chr_size];
-            return *cell(s.chr_ram, addr & 0x1FFF);
+            return s.chr_ram[goff(addr & 0x1FFF)];
         }
         if (addr < 0x3F00) {
             if (addr >= 0x3000) addr -= 0x1000;
-            return *cell(s.nametable, nt_index(addr));
+            return s.nametable[goff(nt_index(addr))];
         }
-        return *cell(s.palette, pal_index(addr));
+        return s.palette[goff(pal_index(addr))];
     }
-    __device__ void vram_wr(std::uint32_t addr, std::uint32_t v) const {
+    __device__ void vram_wr(std::uint32_t addr, std::uint32_t val) const {
         addr &= 0x3FFF;
         if (addr < 0x2000) {
-            if (s.chr_size == 0) *cell(s.chr_ram, addr & 0x1FFF) = static_cast<std::uint8_t>(v);
+            if (s.chr_size == 0) s.chr_ram[goff(addr & 0x1FFF)] = static_cast<std::uint8_t>(val);
             return;
         }
         if (addr < 0x3F00) {
             if (addr >= 0x3000) addr -= 0x1000;
-            *cell(s.nametable, nt_index(addr)) = static_cast<std::uint8_t>(v);
+            s.nametable[goff(nt_index(addr))] = static_cast<std::uint8_t>(val);
             return;
         }
-        *cell(s.palette, pal_index(addr)) = static_cast<std::uint8_t>(v);
+        s.palette[goff(pal_index(addr))] = static_cast<std::uint8_t>(val);
     }
 
-    // ---- I/O space $2000-$7FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
-    //      controller.hpp:20-47) -------------------------------------------------
+    // ---- I/O space $2000-$5FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
+    //      controller.hpp:20-47) ----------------------------------------------------
     __device__ std::uint32_t io_rd(std::uint32_t addr) {
-        const std::uint32_t e = env;
         if (addr < 0x4000) {
-            switch (addr & 7) {
-                case 2: {
-                    const std::uint32_t val = (status & 0xE0) | (s.open_bus[e] & 0x1F);
-                    status &= 0x7F;
-                    nmi = 0;
-                    s.w[e] = 0;
-                    s.open_bus[e] = static_cast<std::uint8_t>(val);
-                    return val;
-                }
-                case 4:
-                    return *cell(s.oam, s.oam_addr[e]);
-                case 7: {
-                    const std::uint32_t va = s.v[e] & 0x3FFF;
-                    std::uint32_t val;
-                    if (va >= 0x3F00) {
-                        val = vram_rd(va);
-                        s.read_buffer[e] = static_cast<std::uint8_t>(vram_rd(va - 0x1000));
-                    } else {
-                        val = s.read_buffer[e];
-                        s.read_buffer[e] = static_cast<std::uint8_t>(vram_rd(va));
-                    }
-                    s.v[e] = static_cast<std::uint16_t>(s.v[e] + ((ctrl & 0x04) ? 32 : 1));
-                    s.open_bus[e] = static_cast<std::uint8_t>(val);
-                    return val;
-                }
-                default:
-                    return s.open_bus[e];
+            const std::uint32_t reg = addr & 7;
+            if (reg == 2) {
+                const std::uint32_t val = (status & 0xE0) | (open_bus & 0x1F);
+                status &= 0x7F;
+                nmi = 0;
+                w = 0;
+                open_bus = val;
+                return val;
             }
+            if (reg == 4) return s.oam[goff(oam_addr)];
+            if (reg == 7) {
+                const std::uint32_t va = v & 0x3FFF;
+                std::uint32_t val;
+                if (va >= 0x3F00) {
+                    val = vram_rd(va);
+                    read_buffer = vram_rd(va - 0x1000);
+                } else {
+                    val = read_buffer;
+                    read_buffer = vram_rd(va);
+                }
+                v = (v + ((ctrl & 0x04) ? 32u : 1u)) & 0xFFFF;
+                open_bus = val;
+                return val;
+            }
+            return open_bus;
         }
         if (addr == 0x4016) {
-            if (s.strobe[e]) return 0x40 | (s.c1_buttons[e] & 1);
+            if (strobe) return 0x40 | (c1_buttons & 1);
             std::uint32_t bit = 1;
-            const std::uint32_t n = s.c1_count[e];
-            if (n < 8) {
-                const std::uint32_t sh = s.c1_shift[e];
-                bit = sh & 1;
-                s.c1_shift[e] = static_cast<std::uint8_t>(sh >> 1);
-                s.c1_count[e] = static_cast<std::uint8_t>(n + 1);
+            if (c1_count < 8) {
+                bit = c1_shift & 1;
+                c1_shift >>= 1;
+                ++c1_count;
             }
             return 0x40 | bit;
         }
         if (addr == 0x4017) {
-            if (s.strobe[e]) return 0x40;
-            const std::uint32_t n = s.c2_count[e];
-            if (n < 8) {
-                s.c2_count[e] = static_cast<std::uint8_t>(n + 1);
+            if (strobe) return 0x40;
+            if (c2_count < 8) {
+                ++c2_count;
                 return 0x40;
             }
             return 0x41;
         }
-        if (addr < 0x4018) return *cell(s.apu_io, addr - 0x4000);
-        if (addr >= 0x6000) return *cell(s.prg_ram, addr - 0x6000);
+        if (addr < 0x4018) return s.apu_io[goff(addr - 0x4000)];
         return 0;
     }
 
     __device__ void ppu_wr(std::uint32_t reg, std::uint32_t val) {
-        const std::uint32_t e = env;
-        s.open_bus[e] = static_cast<std::uint8_t>(val);
+        open_bus = val;
         switch (reg) {
             case 0:
                 if ((val & 0x80) && !(ctrl & 0x80) && (status & 0x80)) nmi = 1;
                 ctrl = val;
-                s.t[e] = static_cast<std::uint16_t>((s.t[e] & 0xF3FF) | ((val & 0x03) << 10));
+                t = (t & 0xF3FF) | ((val & 0x03) << 10);
                 break;
             case 1:
                 mask = val;
                 break;
             case 3:
-                s.oam_addr[e] = static_cast<std::uint8_t>(val);
+                oam_addr = val;
                 break;
-            case 4: {
-                const std::uint32_t oa = s.oam_addr[e];
-                *cell(s.oam, oa) = static_cast<std::uint8_t>(val);
-                s.oam_addr[e] = static_cast<std::uint8_t>(oa + 1);
+            case 4:
+                s.oam[goff(oam_addr)] = static_cast<std::uint8_t>(val);
+                oam_addr = (oam_addr + 1) & 0xFF;
                 break;
-            }
             case 5:
-                if (!s.w[e]) {
-                    s.fine_x[e] = static_cast<std::uint8_t>(val & 7);
-                    s.t[e] = static_cast<std::uint16_t>((s.t[e] & 0xFFE0) | (val >> 3));
-                    s.scroll_x[e] = static_cast<std::uint8_t>(val);
-                    s.w[e] = 1;
+                if (!w) {
+                    fine_x = val & 7;
+                    t = (t & 0xFFE0) | (val >> 3);
+                    scroll_x = val;
+                    w = 1;
                 } else {
-                    std::uint32_t t = (s.t[e] & 0x8FFF) | ((val & 0x07) << 12);
+                    t = (t & 0x8FFF) | ((val & 0x07) << 12);
                     t = (t & 0xFC1F) | ((val & 0xF8) << 2);
-                    s.t[e] = static_cast<std::uint16_t>(t);
-                    s.scroll_y[e] = static_cast<std::uint8_t>(val);
-                    s.w[e] = 0;
+                    scroll_y = val;
+                    w = 0;
                 }
                 break;
             case 6:
-                if (!s.w[e]) {
-                    s.t[e] = static_cast<std::uint16_t>((s.t[e] & 0x00FF) | ((val & 0x3F) << 8));
-                    s.w[e] = 1;
+                if (!w) {
+                    t = (t & 0x00FF) | ((val & 0x3F) << 8);
+                    w = 1;
                 } else {
-                    const std::uint16_t t = static_cast<std::uint16_t>((s.t[e] & 0x7F00) | val);
-                    s.t[e] = t;
-                    s.v[e] = t;
-                    s.w[e] = 0;
+                    t = (t & 0x7F00) | val;
+                    v = t;
+                    w = 0;
                 }
                 break;
-            case 7: {
-                const std::uint32_t va = s.v[e];
-                vram_wr(va, val);
-                s.v[e] = static_cast<std::uint16_t>(va + ((ctrl & 0x04) ? 32 : 1));
+            case 7:
+                vram_wr(v, val);
+                v = (v + ((ctrl & 0x04) ? 32u : 1u)) & 0xFFFF;
                 break;
-            }
             default:
                 break;
         }
     }
 
-    // OAM DMA ($4014): 256 bus reads into OAM from OAMADDR, +513 CPU cycles
-    // after the instruction (console.hpp:191-197).  Pages below $20 are plain
-    // RAM; higher pages go through the full bus with its side effects.
-    __device__ void oam_dma(std::uint32_t page) {
-        const std::uint32_t oa = s.oam_addr[env];
-        const std::uint32_t base = page << 8;
-        if (page < 0x20) {
-            for (std::uint32_t i = 0; i < 256; ++i) *cell(s.oam, (oa + i) & 0xFF) = static_cast<std::uint8_t>(ram_rd(base + i));
-        } else {
-            for (std::uint32_t i = 0; i < 256; ++i) {
-                const std::uint32_t ad = (base + i) & 0xFFFF;
-                std::uint32_t v;
-                v = rd(ad);
-                *cell(s.oam, (oa + i) & 0xFF) = static_cast<std::uint8_t>(v);
-            }
-        }
-        dma += 513;
-    }
-
-    __device__ void io_wr(std::uint32_t addr, std::uint32_t val) {
-        const std::uint32_t e = env;
+    // Returns the extra PPU dots the write costs (OAM DMA: 513 CPU cycles).
+    __device__ std::uint32_t io_wr(std::uint32_t addr, std::uint32_t val) {
         if (addr < 0x4000) {
             ppu_wr(addr & 7, val);
-            return;
-        }
-        if (addr == 0x4014) {
-            *cell(s.apu_io, 0x14) = static_cast<std::uint8_t>(val);
-            oam_dma(val);
-            return;
-        }
-        if (addr == 0x4016) {
-            *cell(s.apu_io, 0x16) = static_cast<std::uint8_t>(val);
-            const std::uint32_t next = val & 1;
-            if (next || s.strobe[e]) {
-                s.c1_shift[e] = s.c1_buttons[e];
-                s.c1_count[e] = 0;
-                s.c2_count[e] = 0;
-            }
-            s.strobe[e] = static_cast<std::uint8_t>(next);
-            return;
-        }
-        if (addr < 0x4018) {
-            *cell(s.apu_io, addr - 0x4000) = static_cast<std::uint8_t>(val);
-            return;
-        }
-        if (addr >= 0x6000) *cell(s.prg_ram, addr - 0x6000) = static_cast<std::uint8_t>(val);
-    }
-
-    // ---- CPU bus -------------------------------------------------------------
-    __device__ __forceinline__ static bool is_io(std::uint32_t addr) { return addr >= 0x2000 && addr < 0x8000; }
-    __device__ __forceinline__ std::uint32_t rd(std::uint32_t addr) {
-        if (is_io(addr)) return io_rd(addr);
-        return *gptr(addr);
-    }
-    __device__ __forceinline__ void wr(std::uint32_t addr, std::uint32_t v) {
-        if (addr < 0x2000) {
-            ram_wr(addr, v);
-        } else if (addr < 0x8000) {
-            io_wr(addr, v);
-        }
-    }
-
-    // ---- one instruction (console.hpp:108-135 + cpu.hpp:377-730) -------------
-    // Returns the PPU dots it accounts for (3 per CPU cycle, NMI and DMA
-    // included); `op_out`/`pc_out` identify the executed opcode.
-    __device__ __forceinline__ std::uint32_t exec(std::uint32_t& op_out, std::uint32_t& pc_out) {
-        std::uint32_t cyc = 0;
-        if (nmi) {  // cpu.hpp:112-123, taken before the instruction
-            nmi = 0;
-            *gptr(0x100 | sp) = static_cast<std::uint8_t>(pc >> 8);
-            *gptr(0x100 | ((sp - 1) & 0xFF)) = static_cast<std::uint8_t>(pc);
-            *gptr(0x100 | ((sp - 2) & 0xFF)) = static_cast<std::uint8_t>((p & ~0x10u) | 0x20u);
-            sp = (sp - 3) & 0xFF;
-            p |= 0x24;
-            pc = nmi_vec;
-            cyc = 7;
-        }
-        pc_out = pc;
-
-        // Fetch the opcode and two operand bytes: two aligned LDS dwords.
-        std::uint32_t op, b1, b2;
-        if (pc >= 0x8000u && pc <= 0xFFFDu) {
-            const std::uint32_t off = pc & 0x7FFF;
-            const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(lds);
-            const std::uint32_t bytes = __builtin_amdgcn_alignbyte(w[(off >> 2) + 1], w[off >> 2], off & 3);
-            op = bytes & 0xFF;
-            b1 = (bytes >> 8) & 0xFF;
-            b2 = (bytes >> 16) & 0xFF;
-        } else {  // code outside PRG ROM: exact bus reads, in order
-            op = rd(pc);
-            const std::uint32_t len = static_cast<std::uint32_t>(
-                reinterpret_cast<const std::uint64_t*>(lds + kLdsMicro)[op] >> 58) & 3;
-            b1 = len >= 2 ? rd((pc + 1) & 0xFFFF) : 0u;
-            b2 = len >= 3 ? rd((pc + 2) & 0xFFFF) : 0u;
-        }
-        op_out = op;
-        const std::uint64_t m = reinterpret_cast<const std::uint64_t*>(lds + kLdsMicro)[op];
-        // Zero-page pointers for (zp,X) and (zp),Y, read before the decode is known.
-        const std::uint32_t px = (b1 + x) & 0xFF;
-        const std::uint32_t ptr_x = ram_rd(px) | (ram_rd((px + 1) & 0xFF) << 8);
-        const std::uint32_t ptr_y = ram_rd(b1) | (ram_rd((b1 + 1) & 0xFF) << 8);
-
-        const std::uint32_t lo = static_cast<std::uint32_t>(m);
-        const std::uint32_t hi = static_cast<std::uint32_t>(m >> 32);
-        const std::uint32_t mode = lo & 15;
-        const std::uint32_t kind = (lo >> 8) & 3;
-        if (kind == mc::KILLEGAL) {
-            fault |= 1;
             return 0;
         }
-        cyc += (lo >> 4) & 7;
-
-        // Effective address.
-        const std::uint32_t abs = b1 | (b2 << 8);
-        const std::uint32_t base = mode == mc::INDX ? ptr_x : (mode == mc::INDY ? ptr_y : abs);
-        constexpr std::uint32_t kUsesX = (1u << mc::ZPX) | (1u << mc::ABSX);
-        constexpr std::uint32_t kUsesY = (1u << mc::ZPY) | (1u << mc::ABSY) | (1u << mc::INDY);
-        constexpr std::uint32_t kZeroPage = (1u << mc::ZP) | (1u << mc::ZPX) | (1u << mc::ZPY);
-        const std::uint32_t idx = ((kUsesX >> mode) & 1) ? x : (((kUsesY >> mode) & 1) ? y : 0u);
-        const bool zpm = (kZeroPage >> mode) & 1;
-        const std::uint32_t addr = zpm ? ((b1 + idx) & 0xFF) : ((base + idx) & 0xFFFF);
-        cyc += ((lo >> 7) & 1) & ((!zpm && ((base ^ addr) >> 8) != 0) ? 1u : 0u);
-
-        // Operand: one FLAT load for RAM/PRG lanes, the I/O path for the rest.
-        const bool rd_op = (lo >> 13) & 1;
-        const bool io = is_io(addr);
-        std::uint8_t* const ap = gptr(addr);
-        std::uint32_t M = b1;
-        if (rd_op && !io) M = *ap;
-        if (rd_op && io) M = io_rd(addr);
-
-        // Datapath: adder / logic / shifter.
-        const std::uint32_t rsel = (lo >> 10) & 3;
-        const std::uint32_t R = rsel == 0 ? a : (rsel == 1 ? x : (rsel == 2 ? y : sp));
-        const std::uint32_t xa = ((lo >> 12) & 1) ? M : R;
-        const std::uint32_t xb = ((lo >> 19) & 1) ? (M ^ (((lo >> 20) & 1) ? 0xFFu : 0u))
-                                                  : (((lo >> 21) & 1) ? 0xFFu : 0u);
-        const std::uint32_t csel = (lo >> 22) & 3;
-        const std::uint32_t cf = p & 1;
-        const std::uint32_t cin = csel == mc::CFLAG ? cf : csel;
-        const std::uint32_t sum = xa + xb + cin;
-        const std::uint32_t land = R & M, lxor = R ^ M;
-        const std::uint32_t lsel = (lo >> 17) & 3;
-        const std::uint32_t lres = lsel == mc::LAND ? land : (lsel == mc::LOR ? (land | lxor) : lxor);
-        const bool rot = (lo >> 25) & 1;
-        const bool right = (lo >> 24) & 1;
-        const std::uint32_t sres = right ? ((xa >> 1) | (rot ? cf << 7 : 0u)) : (((xa << 1) | (rot ? cf : 0u)) & 0xFF);
-        const std::uint32_t scarry = right ? (xa & 1) : (xa >> 7);
-        const std::uint32_t unit = (lo >> 15) & 3;
-        const std::uint32_t r = unit == mc::UADD ? (sum & 0xFF) : (unit == mc::ULOGIC ? lres : sres);
-        const std::uint32_t carry = unit == mc::USHIFT ? scarry : ((sum >> 8) & 1);
-        const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
-        const bool bit_rule = (lo >> 29) & 1;
-        const std::uint32_t f = ((bit_rule ? M : r) & 0x80) | (bit_rule ? (M & 0x40) : ovf) | (r == 0 ? 2u : 0u) | carry;
-        const std::uint32_t fmask = ((lo >> 30) | (hi << 2)) & 0xFF;
-        const std::uint32_t pand = (hi >> 6) & 0xFF;
-        const std::uint32_t por = (hi >> 14) & 0xFF;
-        p = ((((p & ~fmask) | (f & fmask)) & pand) | por | 0x20) & 0xFF;
-
-        // Register write-back and memory write.
-        const std::uint32_t dst = (lo >> 26) & 7;
-        a = dst == mc::DA ? r : a;
-        x = dst == mc::DX ? r : x;
-        y = dst == mc::DY ? r : y;
-        sp = dst == mc::DSP ? r : sp;
-        const bool wr_op = (lo >> 14) & 1;
-        if (wr_op && addr < 0x2000) *ap = static_cast<std::uint8_t>(r);
-        if (wr_op && io) io_wr(addr, r);
-
-        // Next PC: fall through, branch, or control transfer.
-        std::uint32_t next = (pc + ((hi >> 26) & 3)) & 0xFFFF;
-        if (kind == mc::KBRANCH) {
-            const std::uint32_t pos = (0x1067u >> ((op >> 6) * 4)) & 0xF;
-            const bool taken = ((p >> pos) & 1) == ((op >> 5) & 1);
-            const std::uint32_t target = (next + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
-            cyc += taken ? (1u + (((next ^ target) >> 8) != 0 ? 1u : 0u)) : 0u;
-            next = taken ? target : next;
-        } else if (kind == mc::KCTRL) {
-            // Stack unit: JSR/BRK/PHA/PHP push, RTS/RTI/PLA/PLP pull
-            // (cpu.hpp:394-402, 603-606, 666-694).
-            const std::uint32_t c = (hi >> 22) & 15;
-            constexpr std::uint32_t kPushes =
-                (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) | (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
-            constexpr std::uint32_t kPulls =
-                (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) | (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
-            const std::uint32_t npush = (kPushes >> (2 * c)) & 3;
-            const std::uint32_t npull = (kPulls >> (2 * c)) & 3;
-            const std::uint32_t ret = (pc + 2) & 0xFFFF;
-            const std::uint32_t pb = p | 0x30;
-            const std::uint32_t v0 = c == mc::PHA ? a : (c == mc::PHP ? pb : (ret >> 8));
-            if (npush >= 1) *gptr(0x100 | sp) = static_cast<std::uint8_t>(v0);
-            if (npush >= 2) *gptr(0x100 | ((sp - 1) & 0xFF)) = static_cast<std::uint8_t>(ret);
-            if (npush >= 3) *gptr(0x100 | ((sp - 2) & 0xFF)) = static_cast<std::uint8_t>(pb);
-            std::uint32_t w0 = 0, w1 = 0, w2 = 0;
-            if (npull >= 1) w0 = *gptr(0x100 | ((sp + 1) & 0xFF));
-            if (npull >= 2) w1 = *gptr(0x100 | ((sp + 2) & 0xFF));
-            if (npull >= 3) w2 = *gptr(0x100 | ((sp + 3) & 0xFF));
-            sp = (sp - npush + npull) & 0xFF;
-            const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
-            p = (c == mc::RTI || c == mc::PLP) ? pulled_p : (c == mc::BRK ? (p | 0x24) : p);
-            if (c == mc::PLA) {
-                a = w0;
-                p = (p & 0x7D) | (a & 0x80) | (a == 0 ? 2u : 0u) | 0x20;
-            }
-            next = (c == mc::JMPA || c == mc::JSR) ? abs
-                 : c == mc::RTS ? (((w0 | (w1 << 8)) + 1) & 0xFFFF)
-                 : c == mc::RTI ? (w1 | (w2 << 8))
-                 : c == mc::BRK ? brk_vec : next;
-            if (c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
-                const std::uint32_t l = rd(abs);
-                next = l | (rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
-            }
+        if (addr >= 0x4018) return 0;
+        s.apu_io[goff(addr - 0x4000)] = static_cast<std::uint8_t>(val);
+        if (addr == 0x4014) {
+            dma = 0x100 | val;  // copied by the wave right after this instruction
+            return 3 * 513;
         }
-        pc = next;
-        cyc += dma;
-        dma = 0;
-        cycles += cyc;
-        return cyc * 3;
+        if (addr == 0x4016) {
+            const std::uint32_t next = val & 1;
+            if (next || strobe) {
+                c1_shift = c1_buttons;
+                c1_count = 0;
+                c2_count = 0;
+            }
+            strobe = next;
+        }
+        return 0;
     }
 
-    // ---- PPU timing (ppu.hpp:46-76, 136-147) ---------------------------------
-    // Dots until the next timing event (sprite-0 dot, vblank, pre-render, frame
-    // end) from the current position.  Written with unconditional signed
-    // differences: the form with unsigned subtractions guarded by `ev > c` is
-    // mis-compiled for gfx950 by ROCm 7.2's clang (the guarded pre-render term
-    // is dropped), which the parity tests caught.
-    __device__ __forceinline__ std::uint32_t to_event() const {
-        const std::int32_t c = static_cast<std::int32_t>(frame_dot);
-        std::int32_t d = static_cast<std::int32_t>(kFrameDots) - c;
-        const std::int32_t s0 = static_cast<std::int32_t>(kSprite0Dot) - c;
-        const std::int32_t vb = static_cast<std::int32_t>(kVblankDot) - c;
-        const std::int32_t pr = static_cast<std::int32_t>(kPreRenderDot) - c;
-        d = (s0 > 0 && s0 < d) ? s0 : d;
-        d = (vb > 0 && vb < d) ? vb : d;
-        d = (pr > 0 && pr < d) ? pr : d;
-        return static_cast<std::uint32_t>(d);
+    // ---- CPU bus (console.hpp:49-101) --------------------------------------------
+    __device__ std::uint32_t bus_rd(std::uint32_t addr) {
+        if (addr < 0x2000) return ram_rd(addr & 0x7FF);
+        if (addr >= 0x8000) return lds[addr & 0x7FFF];
+        if (addr >= 0x6000) return s.ram[goff(addr - 0x5800)];
+        return io_rd(addr);
     }
 
-    // Advance the PPU by `dots` (< one frame past the next frame end) and apply
-    // every event crossed, in order.  Returns frames completed (0 or 1).
+    // ---- PPU timing (ppu.hpp:46-76) -------------------------------------------------
+    // Advance by `dots` (less than one frame past the next frame end), applying
+    // every event crossed in order.  Returns frames completed (0 or 1).
     __device__ __forceinline__ std::uint32_t settle(std::uint32_t dots) {
         const std::uint32_t start = frame_dot, end = start + dots;
         const std::uint32_t fc = end >= kFrameDots ? 1u : 0u;
@@ -531,199 +325,405 @@ struct Lane {
             }
         }
         frame_dot = end - fc * kFrameDots;
-        frames += fc;
         return fc;
     }
 };
 
-// ---- the step kernel ------------------------------------------------------------
-// Launched with T = blockDim.x threads (64 or 256) and lds_bytes(T) bytes of
-// dynamic LDS.
-template <int kStats>
-__global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uint32_t frameskip,
-                                                         std::uint32_t max_instr, std::uint32_t auto_reset) {
-    extern __shared__ __attribute__((aligned(16))) std::uint8_t lds_raw[];
-    const std::uint32_t T = blockDim.x, tid = threadIdx.x;
-    {
-        // PRG ROM (16 KB images are mirrored so every fetch can use & 0x7FFF)
-        // and the microcode table.
-        const std::uint32_t bytes = s.prg_mask + 1;
+// ---- the step kernel ---------------------------------------------------------------
+// kStats: 0 none, 1 per-console counters, 2 counters + opcode/PC histograms.
+// kFull: all console RAM in LDS.  kBudget: the per-frame instruction budget can
+// bind (a frame always completes within 14,891 instructions, since every
+// instruction advances the PPU by at least 6 dots).
+template <int kStats, bool kFull, bool kBudget>
+__global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32_t frameskip, std::uint32_t max_instr,
+                                                      std::uint32_t auto_reset, std::uint32_t lane_bits) {
+    using C = Console<kFull>;
+    const std::uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const std::uint32_t L = 1u << lane_bits;
+    const std::uint32_t slot = wave * L + lane;
+    const std::uint32_t env = xcd_block(blockIdx.x, gridDim.x) * (4u * L) + slot;
+    const bool mine = lane < L && env < s.n;
+
+    {   // PRG ROM (a 16 KB image mirrored to 32 KB) and the microcode table.
+        const std::uint32_t words = (s.prg_mask + 1) / 16;
         const uint4* src = reinterpret_cast<const uint4*>(s.prg_rom);
-        uint4* dst = reinterpret_cast<uint4*>(lds_raw);
-        for (std::uint32_t i = tid; i < kPrgRomMax / 16; i += T) dst[i] = src[i & ((bytes / 16) - 1)];
-        if (tid < 1) dst[kPrgRomMax / 16] = src[0];
-        std::uint64_t* micro = reinterpret_cast<std::uint64_t*>(lds_raw + kLdsMicro);
-        for (std::uint32_t i = tid; i < 256; i += T) micro[i] = c_micro[i];
+        uint4* dst = reinterpret_cast<uint4*>(lds);
+        for (std::uint32_t i = tid; i < kPrgRomMax / 16; i += kBlock) dst[i] = src[i & (words - 1)];
+        reinterpret_cast<uint4*>(lds + kLdsMicro)[tid] = c_micro[tid];
     }
-    const std::uint32_t env = xcd_block(blockIdx.x, gridDim.x) * T + tid;
-    const bool live = env < s.n;
-    const std::uint32_t stk_base = kLdsZp + kZpBytes * T;
-    std::uint32_t* lds32 = reinterpret_cast<std::uint32_t*>(lds_raw);
-    if (live) {
-        // Stage this console's zero page and stack top into LDS.
+    const std::uint32_t base = kLdsRam + (lane < L ? slot : 0u) * C::kStride;
+    const std::uint32_t P = s.pitch;
+    if (mine) {  // this console's RAM rows that live in LDS
         const std::uint8_t* g = s.ram + env;
-        const std::size_t P = s.pitch;
-        for (std::uint32_t k = 0; k < kZpBytes / 4; ++k) {
-            const std::size_t a0 = 4 * k;
-            lds32[kLdsZp / 4 + k * T + tid] = g[a0 * P] | (g[(a0 + 1) * P] << 8) | (g[(a0 + 2) * P] << 16) |
-                                              (static_cast<std::uint32_t>(g[(a0 + 3) * P]) << 24);
-        }
-        for (std::uint32_t k = 0; k < kStackBytes / 4; ++k) {
-            const std::size_t a0 = kStackLo + 4 * k;
-            lds32[stk_base / 4 + k * T + tid] = g[a0 * P] | (g[(a0 + 1) * P] << 8) | (g[(a0 + 2) * P] << 16) |
-                                                (static_cast<std::uint32_t>(g[(a0 + 3) * P]) << 24);
+        auto stage = [&](std::uint32_t ra, std::uint32_t at) {
+            const std::size_t r = ra;
+            reinterpret_cast<std::uint32_t*>(lds + base + at)[0] =
+                g[r * P] | (g[(r + 1) * P] << 8) | (g[(r + 2) * P] << 16) | (static_cast<std::uint32_t>(g[(r + 3) * P]) << 24);
+        };
+        if (kFull) {
+            for (std::uint32_t ra = 0; ra < kRamBytes; ra += 4) stage(ra, ra);
+        } else {
+            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) stage(ra, ra);
+            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, ra - 0x80);
         }
     }
     __syncthreads();
-    if (!live) return;
 
-    Lane L{s, lds_raw, s.ram + env, env, s.pitch, 4 * T, 4 * tid, stk_base};
-    L.nmi_vec = lds_raw[0x7FFA] | (lds_raw[0x7FFB] << 8);
-    L.brk_vec = lds_raw[0x7FFE] | (lds_raw[0x7FFF] << 8);
-    L.pc = s.pc[env]; L.a = s.a[env]; L.x = s.x[env]; L.y = s.y[env]; L.sp = s.sp[env]; L.p = s.p[env];
-    L.cycles = s.cycles[env];
-    L.frame_dot = s.frame_dot[env]; L.status = s.status[env]; L.ctrl = s.ctrl[env]; L.mask = s.mask[env];
-    L.nmi = s.nmi_pending[env];
-    L.frames = 0; L.dma = 0; L.fault = s.fault[env];
-
-    // The pad reads this step's mask; a high strobe re-latches immediately
-    // (controller.hpp:20-25).
-    const std::uint32_t buttons = s.actions[env];
-    s.c1_buttons[env] = static_cast<std::uint8_t>(buttons);
-    if (s.strobe[env]) {
-        s.c1_shift[env] = static_cast<std::uint8_t>(buttons);
-        s.c1_count[env] = 0;
+    C c{s, mine ? env : 0u, base, P};
+    c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
+    c.brk_vec = lds[0x7FFE] | (lds[0x7FFF] << 8);
+    std::uint32_t frames_left = 0, fd0 = 0;
+    if (mine) {
+        c.pc = s.pc[env];
+        c.regs = s.a[env] | (s.x[env] << 8) | (s.y[env] << 16) | (static_cast<std::uint32_t>(s.sp[env]) << 24);
+        c.p = s.p[env];
+        c.frame_dot = s.frame_dot[env]; c.status = s.status[env]; c.ctrl = s.ctrl[env]; c.mask = s.mask[env];
+        c.nmi = s.nmi_pending[env];
+        c.oam_addr = s.oam_addr[env]; c.open_bus = s.open_bus[env]; c.read_buffer = s.read_buffer[env];
+        c.v = s.v[env]; c.t = s.t[env]; c.fine_x = s.fine_x[env]; c.w = s.w[env];
+        c.scroll_x = s.scroll_x[env]; c.scroll_y = s.scroll_y[env];
+        // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
+        c.c1_buttons = s.actions[env];
+        c.c1_shift = s.c1_shift[env]; c.c1_count = s.c1_count[env]; c.strobe = s.strobe[env];
+        c.c2_count = s.c2_count[env];
+        if (c.strobe) {
+            c.c1_shift = c.c1_buttons;
+            c.c1_count = 0;
+        }
+        c.fault = s.fault[env];
+        frames_left = c.fault ? 0u : frameskip;
+    } else {
+        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.frame_dot = 0; c.status = 0; c.ctrl = 0; c.mask = 0; c.nmi = 0;
+        c.oam_addr = 0; c.open_bus = 0; c.read_buffer = 0; c.v = 0; c.t = 0; c.fine_x = 0; c.w = 0;
+        c.scroll_x = 0; c.scroll_y = 0; c.c1_buttons = 0; c.c1_shift = 0; c.c1_count = 0; c.strobe = 0;
+        c.c2_count = 0; c.fault = 0;
     }
-
-    std::uint32_t frames_left = L.fault ? 0u : frameskip;
-    std::uint32_t in_frame = 0, pending = 0, horizon = L.to_event();
+    c.dma = 0;
+    fd0 = c.frame_dot;
+    std::uint32_t horizon = to_event(c.frame_dot);
+    std::int32_t left = static_cast<std::int32_t>(horizon);
+    std::uint32_t frames = 0, in_frame = 0, budget_hits = 0;
     std::uint64_t instructions = 0;
-    std::uint32_t budget_hits = 0;
-    while (frames_left != 0) {
-        if (pending >= horizon) {
-            const std::uint32_t fc = L.settle(pending);
-            pending = 0;
-            horizon = L.to_event();
-            if (fc) {
-                --frames_left;
-                in_frame = 0;
-                continue;
-            }
-        }
-        std::uint32_t op, pc0;
-        const std::uint32_t dots = L.exec(op, pc0);
-        if (L.fault) break;
-        pending += dots;
-        ++in_frame;
-        ++instructions;
-        if constexpr (kStats == 2) {
-            atomicAdd(&s.prof_opcodes[op], 1ull);
-            atomicAdd(&s.prof_pcs[pc0], 1ull);
-        }
-        // Idle loop (JMP to itself): the console repeats 3-cycle jumps until the
-        // next timing event is crossed; account for them in one go.
-        const std::int32_t gap = static_cast<std::int32_t>(horizon) - static_cast<std::int32_t>(pending);
-        if (op == 0x4C && L.pc == pc0 && gap > 0) {
-            const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame);
-            const std::int32_t want = (gap + 8) / 9;
-            const std::uint32_t k = static_cast<std::uint32_t>(want < room ? want : room);
-            pending += 9 * k;
-            L.cycles += 3ull * k;
-            in_frame += k;
-            instructions += k;
-            if constexpr (kStats == 2) {
-                atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
-                atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
-            }
-        }
-        if (in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
-            const std::uint32_t fc = L.settle(pending);
-            pending = 0;
-            horizon = L.to_event();
-            budget_hits += fc ? 0u : 1u;
-            --frames_left;
-            in_frame = 0;
-        }
-    }
-    if (pending != 0) L.settle(pending);
+    bool active = frames_left != 0;
 
-    // Write the staged zero page and stack top back to HBM.
+    while (__ballot(active) != 0) {
+        if (active) {
+            std::uint32_t dots = 0;
+            if (c.nmi) {  // NMI entry before the instruction (cpu.hpp:112-123, console.hpp:111-115)
+                c.nmi = 0;
+                const std::uint32_t sp = c.regs >> 24;
+                c.ram_wr(0x100 | sp, c.pc >> 8);
+                c.ram_wr(0x100 | ((sp - 1) & 0xFF), c.pc & 0xFF);
+                c.ram_wr(0x100 | ((sp - 2) & 0xFF), (c.p & ~0x10u) | 0x20u);
+                c.regs -= 3u << 24;
+                c.p |= 0x24;
+                c.pc = c.nmi_vec;
+                dots = 21;
+            }
+            // Fetch: opcode and two operand bytes from the PRG image in LDS.
+            const std::uint32_t pc0 = c.pc;
+            const std::uint32_t off = pc0 & 0x7FFF;
+            std::uint32_t op = lds[off], b1 = lds[off + 1], b2 = lds[off + 2];
+            if (pc0 < 0x8000u || pc0 > 0xFFFDu) {  // code outside PRG ROM: bus reads, in order
+                op = c.bus_rd(pc0);
+                const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
+                b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
+                b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
+            }
+            const uint4 m = reinterpret_cast<const uint4*>(lds + kLdsMicro)[op];
+            const std::uint32_t d0 = m.x, d1 = m.y, d2 = m.z, d3 = m.w;
+            const std::uint32_t kind = (d0 >> 10) & 3;
+            if (kind == mc::KILLEGAL) {
+                c.fault |= 1;
+                active = false;
+            } else {
+                // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
+                const std::uint32_t pz = (b1 + (((op & 0x1F) == 0x01) ? ubfe(c.regs, 8, 8) : 0u)) & 0xFF;
+                const std::uint32_t ptr = lds[base + pz] | (lds[base + ((pz + 1) & 0xFF)] << 8);
+                // Effective address.
+                const std::uint32_t abs = b1 | (b2 << 8);
+                const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
+                const std::uint32_t idx = ubfe(c.regs, d0, d1);
+                const std::uint32_t ea = (ebase + idx) & ((d0 & 0x40) ? 0xFFu : 0xFFFFu);
+                dots += ((d0 >> 14) & 31) + 3 * ((((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1);
+                // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
+                // rows, PRG RAM) or the I/O registers.
+                const std::uint32_t ra = ea & 0x7FF;
+                const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
+                const bool ram_lds = is_ram && C::ram_in_lds(ra);
+                const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
+                const bool io = !is_ram && ea < 0x6000;
+                const std::uint32_t laddr = rom ? (ea & 0x7FFF) : (ram_lds ? base + C::ram_lds_off(ra) : base + C::kSpare);
+                const std::uint32_t row = is_ram ? ra : ea - 0x5800;
+                const bool rd = d0 & 0x100, wr = d0 & 0x200;
+                const std::uint32_t ml = lds[laddr];
+                std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
+                if (rd && glob) M = s.ram[c.goff(row)];
+                if (rd && io) M = c.io_rd(ea);
+                // Adder, logic unit and right shifter.
+                const std::uint32_t R = ubfe(c.regs, d2, 8);
+                const std::uint32_t xa = (d1 & 0x20) ? M : R;
+                const std::uint32_t xb = (((d1 & 0x40) ? xa : M) & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
+                const std::uint32_t cf = c.p & 1;
+                const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
+                const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
+                const bool right = d1 & 0x200;
+                const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
+                const std::uint32_t r = right ? sr : ((sum & (d2 >> 24)) | lres);
+                const std::uint32_t carry = right ? (xa & 1) : ((sum >> 8) & 1);
+                const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
+                const std::uint32_t nv = (d0 & 0x800000) ? (M & 0xC0) : ((r & 0x80) | ovf);
+                const std::uint32_t f = nv | ((r & 0xFF) == 0 ? 2u : 0u) | carry;
+                const std::uint32_t fm = d0 >> 24;
+                const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
+                c.p = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
+                // Register write-back.
+                const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
+                c.regs = (c.regs & ~dmask) | ((r << doff) & dmask);
+                // Memory write: LDS RAM (non-writers store to their spare byte),
+                // HBM, or an I/O register.
+                lds[(wr && ram_lds) ? laddr : base + C::kSpare] = static_cast<std::uint8_t>(r);
+                if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
+                if (wr && io) dots += c.io_wr(ea, r & 0xFF);
+                // Next PC: fall through or branch.
+                std::uint32_t next = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
+                const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
+                const std::uint32_t target = (next + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
+                dots += taken ? (((next ^ target) & 0xFF00) ? 6u : 3u) : 0u;
+                next = taken ? target : next;
+                if (kind == mc::KCTRL) {
+                    // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
+                    // JSR/BRK/PHA/PHP push, RTS/RTI/PLA/PLP pull.
+                    const std::uint32_t op_c = (d0 >> 19) & 15;
+                    constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
+                                                      (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
+                    constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
+                                                     (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
+                    const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
+                    const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
+                    const std::uint32_t sp = c.regs >> 24;
+                    const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
+                    const std::uint32_t pb = c.p | 0x30;
+                    const std::uint32_t v0 = op_c == mc::PHA ? (c.regs & 0xFF) : (op_c == mc::PHP ? pb : (ret >> 8));
+                    if (npush >= 1) c.ram_wr(0x100 | sp, v0);
+                    if (npush >= 2) c.ram_wr(0x100 | ((sp - 1) & 0xFF), ret & 0xFF);
+                    if (npush >= 3) c.ram_wr(0x100 | ((sp - 2) & 0xFF), pb);
+                    std::uint32_t w0 = 0, w1 = 0, w2 = 0;
+                    if (npull >= 1) w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
+                    if (npull >= 2) w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
+                    if (npull >= 3) w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
+                    c.regs = (c.regs & 0x00FFFFFFu) | (((sp - npush + npull) & 0xFF) << 24);
+                    const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
+                    c.p = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : (op_c == mc::BRK ? (c.p | 0x24) : c.p);
+                    if (op_c == mc::PLA) {
+                        c.regs = (c.regs & ~0xFFu) | w0;
+                        c.p = (c.p & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
+                    }
+                    next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs
+                         : op_c == mc::RTS ? ((w0 | (w1 << 8)) + 1) & 0xFFFF
+                         : op_c == mc::RTI ? (w1 | (w2 << 8))
+                         : op_c == mc::BRK ? c.brk_vec : next;
+                    if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
+                        const std::uint32_t l = c.bus_rd(abs);
+                        next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
+                    }
+                    // Idle loop (JMP to itself): the console repeats 3-cycle jumps
+                    // until the next timing event; account for them in one go.
+                    const std::int32_t gap = left - static_cast<std::int32_t>(dots);
+                    if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
+                        std::int32_t k = (gap + 8) / 9;
+                        if (kBudget) {
+                            const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
+                            k = k < room ? k : room;
+                        }
+                        dots += 9u * static_cast<std::uint32_t>(k);
+                        in_frame += static_cast<std::uint32_t>(k);
+                        instructions += static_cast<std::uint64_t>(k);
+                        if constexpr (kStats == 2) {
+                            atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
+                            atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
+                        }
+                    }
+                }
+                c.pc = next;
+                if constexpr (kStats == 2) {
+                    atomicAdd(&s.prof_opcodes[op], 1ull);
+                    atomicAdd(&s.prof_pcs[pc0], 1ull);
+                }
+                ++in_frame;
+                ++instructions;
+                left -= static_cast<std::int32_t>(dots);
+                if (left <= 0) {  // a timing event was crossed: settle the PPU
+                    const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
+                    horizon = to_event(c.frame_dot);
+                    left = static_cast<std::int32_t>(horizon);
+                    if (fc) {
+                        ++frames;
+                        in_frame = 0;
+                        if (--frames_left == 0) active = false;
+                    }
+                }
+                if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
+                    const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
+                    horizon = to_event(c.frame_dot);
+                    left = static_cast<std::int32_t>(horizon);
+                    frames += fc;
+                    budget_hits += fc ? 0u : 1u;
+                    in_frame = 0;
+                    if (--frames_left == 0) active = false;
+                }
+            }
+        }
+        // OAM DMA ($4014, console.hpp:191-197): the whole wave copies one
+        // console's 256 bytes at a time, 4 per lane.  RAM, PRG RAM and PRG ROM
+        // pages have no read side effects; I/O pages are read by the console's
+        // own lane through the bus, in order.
+        std::uint64_t req = __ballot(c.dma != 0);
+        while (req != 0) {
+            const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(req)) - 1);
+            req &= req - 1;
+            const std::uint32_t page = __builtin_amdgcn_readlane(c.dma, src) & 0xFF;
+            const std::uint32_t oa = __builtin_amdgcn_readlane(c.oam_addr, src);
+            const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
+            const std::uint32_t e_base = __builtin_amdgcn_readlane(c.base, src);
+            if (page < 0x20 || page >= 0x60) {
+                for (std::uint32_t k = 0; k < 4; ++k) {
+                    const std::uint32_t i = 4 * lane + k;
+                    const std::uint32_t addr = (page << 8) | i;
+                    std::uint32_t val;
+                    if (page < 0x20) {
+                        const std::uint32_t ra = addr & 0x7FF;
+                        val = C::ram_in_lds(ra) ? lds[e_base + C::ram_lds_off(ra)] : s.ram[ra * P + e_env];
+                    } else if (page < 0x80) {
+                        val = s.ram[(addr - 0x5800) * P + e_env];
+                    } else {
+                        val = lds[addr & 0x7FFF];
+                    }
+                    s.oam[((oa + i) & 0xFF) * P + e_env] = static_cast<std::uint8_t>(val);
+                }
+            } else if (lane == src) {
+                // OAMADDR advances with every byte (ppu.hpp:131-134), which a
+                // $2004 read inside the copy observes; it wraps back to `oa`.
+                for (std::uint32_t i = 0; i < 256; ++i) {
+                    c.oam_addr = (oa + i) & 0xFF;
+                    const std::uint32_t val = c.bus_rd((page << 8) | i);
+                    s.oam[c.oam_addr * P + e_env] = static_cast<std::uint8_t>(val);
+                }
+                c.oam_addr = oa;
+            }
+        }
+        c.dma = 0;
+    }
+
+    if (!mine) return;
+    if (left != static_cast<std::int32_t>(horizon)) frames += c.settle(horizon - static_cast<std::uint32_t>(left));
+
+    // Write the LDS-resident RAM rows back to HBM.
     {
         std::uint8_t* g = s.ram + env;
-        const std::size_t P = s.pitch;
-        for (std::uint32_t k = 0; k < kZpBytes / 4; ++k) {
-            const std::uint32_t v = lds32[kLdsZp / 4 + k * T + tid];
-            const std::size_t a0 = 4 * k;
-            g[a0 * P] = static_cast<std::uint8_t>(v);
-            g[(a0 + 1) * P] = static_cast<std::uint8_t>(v >> 8);
-            g[(a0 + 2) * P] = static_cast<std::uint8_t>(v >> 16);
-            g[(a0 + 3) * P] = static_cast<std::uint8_t>(v >> 24);
-        }
-        for (std::uint32_t k = 0; k < kStackBytes / 4; ++k) {
-            const std::uint32_t v = lds32[stk_base / 4 + k * T + tid];
-            const std::size_t a0 = kStackLo + 4 * k;
-            g[a0 * P] = static_cast<std::uint8_t>(v);
-            g[(a0 + 1) * P] = static_cast<std::uint8_t>(v >> 8);
-            g[(a0 + 2) * P] = static_cast<std::uint8_t>(v >> 16);
-            g[(a0 + 3) * P] = static_cast<std::uint8_t>(v >> 24);
+        auto unstage = [&](std::uint32_t ra, std::uint32_t at) {
+            const std::uint32_t v4 = reinterpret_cast<const std::uint32_t*>(lds + base + at)[0];
+            const std::size_t r = ra;
+            g[r * P] = static_cast<std::uint8_t>(v4);
+            g[(r + 1) * P] = static_cast<std::uint8_t>(v4 >> 8);
+            g[(r + 2) * P] = static_cast<std::uint8_t>(v4 >> 16);
+            g[(r + 3) * P] = static_cast<std::uint8_t>(v4 >> 24);
+        };
+        if (kFull) {
+            for (std::uint32_t ra = 0; ra < kRamBytes; ra += 4) unstage(ra, ra);
+        } else {
+            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) unstage(ra, ra);
+            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) unstage(ra, ra - 0x80);
         }
     }
 
-    s.pc[env] = static_cast<std::uint16_t>(L.pc); s.a[env] = static_cast<std::uint8_t>(L.a);
-    s.x[env] = static_cast<std::uint8_t>(L.x); s.y[env] = static_cast<std::uint8_t>(L.y);
-    s.sp[env] = static_cast<std::uint8_t>(L.sp); s.p[env] = static_cast<std::uint8_t>(L.p);
-    s.cycles[env] = L.cycles;
-    s.frame_dot[env] = L.frame_dot; s.frame[env] += L.frames;
-    s.status[env] = static_cast<std::uint8_t>(L.status); s.ctrl[env] = static_cast<std::uint8_t>(L.ctrl);
-    s.mask[env] = static_cast<std::uint8_t>(L.mask); s.nmi_pending[env] = static_cast<std::uint8_t>(L.nmi);
-    s.fault[env] = static_cast<std::uint8_t>(L.fault);
+    s.pc[env] = static_cast<std::uint16_t>(c.pc);
+    s.a[env] = static_cast<std::uint8_t>(c.regs);
+    s.x[env] = static_cast<std::uint8_t>(c.regs >> 8);
+    s.y[env] = static_cast<std::uint8_t>(c.regs >> 16);
+    s.sp[env] = static_cast<std::uint8_t>(c.regs >> 24);
+    s.p[env] = static_cast<std::uint8_t>(c.p);
+    // Every CPU cycle is 3 PPU dots.
+    const std::uint64_t advanced = static_cast<std::uint64_t>(frames) * kFrameDots + c.frame_dot - fd0;
+    s.cycles[env] += advanced / 3;
+    s.frame[env] += frames;
+    s.frame_dot[env] = c.frame_dot;
+    s.status[env] = static_cast<std::uint8_t>(c.status); s.ctrl[env] = static_cast<std::uint8_t>(c.ctrl);
+    s.mask[env] = static_cast<std::uint8_t>(c.mask); s.nmi_pending[env] = static_cast<std::uint8_t>(c.nmi);
+    s.oam_addr[env] = static_cast<std::uint8_t>(c.oam_addr); s.open_bus[env] = static_cast<std::uint8_t>(c.open_bus);
+    s.read_buffer[env] = static_cast<std::uint8_t>(c.read_buffer);
+    s.v[env] = static_cast<std::uint16_t>(c.v); s.t[env] = static_cast<std::uint16_t>(c.t);
+    s.fine_x[env] = static_cast<std::uint8_t>(c.fine_x); s.w[env] = static_cast<std::uint8_t>(c.w);
+    s.scroll_x[env] = static_cast<std::uint8_t>(c.scroll_x); s.scroll_y[env] = static_cast<std::uint8_t>(c.scroll_y);
+    s.c1_buttons[env] = static_cast<std::uint8_t>(c.c1_buttons); s.c1_shift[env] = static_cast<std::uint8_t>(c.c1_shift);
+    s.c1_count[env] = static_cast<std::uint8_t>(c.c1_count); s.strobe[env] = static_cast<std::uint8_t>(c.strobe);
+    s.c2_count[env] = static_cast<std::uint8_t>(c.c2_count);
+    s.fault[env] = static_cast<std::uint8_t>(c.fault);
 
     float reward = 0.0f;
     std::uint32_t done = 1;
-    if (!L.fault) reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
+    if (!c.fault) reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
     s.rewards[env] = reward;
     s.done[env] = static_cast<std::uint8_t>(done);
     if constexpr (kStats != 0) {
         s.stat_instructions[env] = instructions;
-        s.stat_frames[env] = L.frames;
+        s.stat_frames[env] = frames;
         s.stat_budget_hits[env] = budget_hits;
     }
     if (auto_reset && done) {
-        reset_env(s, env, lds_raw);
+        reset_env(s, env, lds);
         seed_baselines(s, env);
     }
 }
 
-}  // namespace
+struct Geometry {
+    std::uint32_t lane_bits, consoles, blocks, lds;
+    bool full;
+};
 
-std::uint32_t step_block_size(std::uint32_t n) {
-    // Small batches: one wave per workgroup spreads consoles over more CUs
-    // (each with its own LDS copy of PRG); large batches: 256-thread groups
-    // share one copy, keeping 4 groups' LDS under 160 KB per CU.
-    return n <= 32768 ? 64u : 256u;
+Geometry geometry(std::uint32_t n) {
+    // One wave per SIMD: 1,024 waves on MI355X's 256 CUs.
+    std::uint32_t lane_bits = 0;
+    while (lane_bits < 6 && (1024u << lane_bits) < n) ++lane_bits;
+    Geometry g{};
+    g.lane_bits = lane_bits;
+    g.consoles = 4u << lane_bits;
+    g.blocks = (n + g.consoles - 1) / g.consoles;
+    g.full = lds_bytes(g.consoles, true) <= kLdsLimit;
+    g.lds = lds_bytes(g.consoles, g.full);
+    return g;
 }
 
-hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr,
-                       bool auto_reset, int stats_mode, hipStream_t stream) {
-    const std::uint32_t T = step_block_size(s.n);
-    const std::uint32_t lds = lds_bytes(T);
-    const dim3 grid((s.n + T - 1) / T), block(T);
-    const std::uint32_t ar = auto_reset ? 1u : 0u;
-    if (stats_mode == 2) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<2>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        step_kernel<2><<<grid, block, lds, stream>>>(s, frameskip, max_instr, ar);
-    } else if (stats_mode == 1) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<1>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        step_kernel<1><<<grid, block, lds, stream>>>(s, frameskip, max_instr, ar);
-    } else {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<0>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        step_kernel<0><<<grid, block, lds, stream>>>(s, frameskip, max_instr, ar);
-    }
+template <int kStats, bool kFull, bool kBudget>
+hipError_t launch_variant(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
+                          std::uint32_t auto_reset, hipStream_t stream) {
+    const void* fn = reinterpret_cast<const void*>(&step_kernel<kStats, kFull, kBudget>);
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(g.lds));
+    if (e != hipSuccess) return e;
+    step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(kBlock), g.lds, stream>>>(s, frameskip, max_instr,
+                                                                                         auto_reset, g.lane_bits);
     return hipGetLastError();
 }
 
+template <int kStats, bool kBudget>
+hipError_t launch_mode(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
+                       std::uint32_t auto_reset, hipStream_t stream) {
+    return g.full ? launch_variant<kStats, true, kBudget>(s, g, frameskip, max_instr, auto_reset, stream)
+                  : launch_variant<kStats, false, kBudget>(s, g, frameskip, max_instr, auto_reset, stream);
+}
+
+}  // namespace
+
+hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, bool auto_reset,
+                       int stats_mode, hipStream_t stream) {
+    const Geometry g = geometry(s.n);
+    const std::uint32_t ar = auto_reset ? 1u : 0u;
+    // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
+    const bool budget = max_instr < 15000;
+    if (stats_mode == 2) return launch_mode<2, true>(s, g, frameskip, max_instr, ar, stream);
+    if (stats_mode == 1) return launch_mode<1, true>(s, g, frameskip, max_instr, ar, stream);
+    return budget ? launch_mode<0, true>(s, g, frameskip, max_instr, ar, stream)
+                  : launch_mode<0, false>(s, g, frameskip, max_instr, ar, stream);
+}
 
 }  // namespace nesle
