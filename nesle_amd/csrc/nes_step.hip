@@ -61,8 +61,16 @@ extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 constexpr std::uint32_t kBlock = 256;           // 4 waves
 constexpr std::uint32_t kLdsMicro = 32768;      // 256 x 16 B
 constexpr std::uint32_t kLdsRam = 32768 + 4096; // console RAM blocks
-constexpr std::uint32_t kSplitStride = 388;     // $0000-$00FF, $0180-$01FF, 4 spare bytes
-constexpr std::uint32_t kFullStride = 2052;     // $0000-$07FF, 4 spare bytes
+// Per-console LDS block: RAM rows, 4 spare bytes, then the PPU/pad registers.
+constexpr std::uint32_t kSplitStride = 412;     // $0000-$00FF, $0180-$01FF, spare, registers
+constexpr std::uint32_t kFullStride = 2076;     // $0000-$07FF, spare, registers
+// Register area offsets (bytes from the start of the area).
+namespace reg {
+constexpr std::uint32_t kCtrl = 0, kMask = 1, kStatus = 2, kOamAddr = 3, kOpenBus = 4, kReadBuffer = 5;
+constexpr std::uint32_t kFineX = 6, kW = 7, kScrollX = 8, kScrollY = 9, kC1Buttons = 10, kC1Shift = 11;
+constexpr std::uint32_t kC1Count = 12, kStrobe = 13, kC2Count = 14, kV = 16, kT = 18, kFrameDot = 20;
+constexpr std::uint32_t kBytes = 24;
+}  // namespace reg
 constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 
 constexpr std::uint32_t lds_bytes(std::uint32_t consoles, bool full) {
@@ -98,21 +106,35 @@ __device__ __forceinline__ std::uint32_t to_event(std::uint32_t fd) {
 template <bool kFull>
 struct Console {
     static constexpr std::uint32_t kStride = kFull ? kFullStride : kSplitStride;
-    static constexpr std::uint32_t kSpare = kFull ? 2048u : 384u;
+    static constexpr std::uint32_t kSpare = kFull ? 2048u : 384u;  // dummy store target
+    static constexpr std::uint32_t kRegs = kSpare + 4;              // register area
 
     const DeviceState& s;
     std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
-    // CPU.
-    std::uint32_t pc, regs, p;
-    // PPU.
-    std::uint32_t frame_dot, status, ctrl, mask, nmi;
-    std::uint32_t oam_addr, open_bus, read_buffer, v, t, fine_x, w, scroll_x, scroll_y;
-    // Pads.
-    std::uint32_t c1_buttons, c1_shift, c1_count, strobe, c2_count;
-    // OAM DMA requested by the current instruction (page | 0x100).
-    std::uint32_t dma;
-    std::uint32_t fault;
+    // Hot state in VGPRs: CPU registers, the NMI latch, a pending OAM DMA
+    // (page | 0x100) and the fault flag.  PPU and pad registers live in the
+    // console's LDS register area (reg::*): only the I/O paths, PPU settlement
+    // and NMI entry touch them.
+    std::uint32_t pc, regs, p, nmi, dma, fault;
+
+    // ---- LDS register area ----------------------------------------------------------
+    __device__ __forceinline__ std::uint32_t r8(std::uint32_t f) const { return lds[base + kRegs + f]; }
+    __device__ __forceinline__ void w8(std::uint32_t f, std::uint32_t v) const {
+        lds[base + kRegs + f] = static_cast<std::uint8_t>(v);
+    }
+    __device__ __forceinline__ std::uint32_t r16(std::uint32_t f) const {
+        return *reinterpret_cast<const std::uint16_t*>(lds + base + kRegs + f);
+    }
+    __device__ __forceinline__ void w16(std::uint32_t f, std::uint32_t v) const {
+        *reinterpret_cast<std::uint16_t*>(lds + base + kRegs + f) = static_cast<std::uint16_t>(v);
+    }
+    __device__ __forceinline__ std::uint32_t r32(std::uint32_t f) const {
+        return *reinterpret_cast<const std::uint32_t*>(lds + base + kRegs + f);
+    }
+    __device__ __forceinline__ void w32(std::uint32_t f, std::uint32_t v) const {
+        *reinterpret_cast<std::uint32_t*>(lds + base + kRegs + f) = v;
+    }
 
     // ---- console RAM ($0000-$07FF, mirrored to $1FFF) -------------------------
     __device__ __forceinline__ static bool ram_in_lds(std::uint32_t ra) {
@@ -121,7 +143,8 @@ struct Console {
     __device__ __forceinline__ static std::uint32_t ram_lds_off(std::uint32_t ra) {
         return kFull ? ra : ra - ((ra >> 1) & 0x80u);
     }
-    __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return row * pitch + env; }
+    // Offset of (row, this console) in an address-major interleaved array.
+    __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return __umul24(row, pitch) + env; }
     __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t ra) const {
         if (ram_in_lds(ra)) return lds[base + ram_lds_off(ra)];
         return s.ram[goff(ra)];
@@ -177,44 +200,49 @@ struct Console {
         if (addr < 0x4000) {
             const std::uint32_t reg = addr & 7;
             if (reg == 2) {
-                const std::uint32_t val = (status & 0xE0) | (open_bus & 0x1F);
-                status &= 0x7F;
+                const std::uint32_t st = r8(reg::kStatus);
+                const std::uint32_t val = (st & 0xE0) | (r8(reg::kOpenBus) & 0x1F);
+                w8(reg::kStatus, st & 0x7F);
                 nmi = 0;
-                w = 0;
-                open_bus = val;
+                w8(reg::kW, 0);
+                w8(reg::kOpenBus, val);
                 return val;
             }
-            if (reg == 4) return s.oam[goff(oam_addr)];
+            if (reg == 4) return s.oam[goff(r8(reg::kOamAddr))];
             if (reg == 7) {
+                const std::uint32_t v = r16(reg::kV);
                 const std::uint32_t va = v & 0x3FFF;
                 std::uint32_t val;
                 if (va >= 0x3F00) {
                     val = vram_rd(va);
-                    read_buffer = vram_rd(va - 0x1000);
+                    w8(reg::kReadBuffer, vram_rd(va - 0x1000));
                 } else {
-                    val = read_buffer;
-                    read_buffer = vram_rd(va);
+                    val = r8(reg::kReadBuffer);
+                    w8(reg::kReadBuffer, vram_rd(va));
                 }
-                v = (v + ((ctrl & 0x04) ? 32u : 1u)) & 0xFFFF;
-                open_bus = val;
+                w16(reg::kV, v + ((r8(reg::kCtrl) & 0x04) ? 32u : 1u));
+                w8(reg::kOpenBus, val);
                 return val;
             }
-            return open_bus;
+            return r8(reg::kOpenBus);
         }
         if (addr == 0x4016) {
-            if (strobe) return 0x40 | (c1_buttons & 1);
+            if (r8(reg::kStrobe)) return 0x40 | (r8(reg::kC1Buttons) & 1);
             std::uint32_t bit = 1;
-            if (c1_count < 8) {
-                bit = c1_shift & 1;
-                c1_shift >>= 1;
-                ++c1_count;
+            const std::uint32_t n = r8(reg::kC1Count);
+            if (n < 8) {
+                const std::uint32_t sh = r8(reg::kC1Shift);
+                bit = sh & 1;
+                w8(reg::kC1Shift, sh >> 1);
+                w8(reg::kC1Count, n + 1);
             }
             return 0x40 | bit;
         }
         if (addr == 0x4017) {
-            if (strobe) return 0x40;
-            if (c2_count < 8) {
-                ++c2_count;
+            if (r8(reg::kStrobe)) return 0x40;
+            const std::uint32_t n = r8(reg::kC2Count);
+            if (n < 8) {
+                w8(reg::kC2Count, n + 1);
                 return 0x40;
             }
             return 0x41;
@@ -223,53 +251,48 @@ struct Console {
         return 0;
     }
 
-    __device__ void ppu_wr(std::uint32_t reg, std::uint32_t val) {
-        open_bus = val;
-        switch (reg) {
-            case 0:
-                if ((val & 0x80) && !(ctrl & 0x80) && (status & 0x80)) nmi = 1;
-                ctrl = val;
-                t = (t & 0xF3FF) | ((val & 0x03) << 10);
-                break;
-            case 1:
-                mask = val;
-                break;
-            case 3:
-                oam_addr = val;
-                break;
-            case 4:
-                s.oam[goff(oam_addr)] = static_cast<std::uint8_t>(val);
-                oam_addr = (oam_addr + 1) & 0xFF;
-                break;
-            case 5:
-                if (!w) {
-                    fine_x = val & 7;
-                    t = (t & 0xFFE0) | (val >> 3);
-                    scroll_x = val;
-                    w = 1;
-                } else {
-                    t = (t & 0x8FFF) | ((val & 0x07) << 12);
-                    t = (t & 0xFC1F) | ((val & 0xF8) << 2);
-                    scroll_y = val;
-                    w = 0;
-                }
-                break;
-            case 6:
-                if (!w) {
-                    t = (t & 0x00FF) | ((val & 0x3F) << 8);
-                    w = 1;
-                } else {
-                    t = (t & 0x7F00) | val;
-                    v = t;
-                    w = 0;
-                }
-                break;
-            case 7:
-                vram_wr(v, val);
-                v = (v + ((ctrl & 0x04) ? 32u : 1u)) & 0xFFFF;
-                break;
-            default:
-                break;
+    __device__ void ppu_wr(std::uint32_t r, std::uint32_t val) {
+        w8(reg::kOpenBus, val);
+        if (r == 0) {
+            const std::uint32_t ctrl = r8(reg::kCtrl);
+            if ((val & 0x80) && !(ctrl & 0x80) && (r8(reg::kStatus) & 0x80)) nmi = 1;
+            w8(reg::kCtrl, val);
+            w16(reg::kT, (r16(reg::kT) & 0xF3FF) | ((val & 0x03) << 10));
+        } else if (r == 1) {
+            w8(reg::kMask, val);
+        } else if (r == 3) {
+            w8(reg::kOamAddr, val);
+        } else if (r == 4) {
+            const std::uint32_t oa = r8(reg::kOamAddr);
+            s.oam[goff(oa)] = static_cast<std::uint8_t>(val);
+            w8(reg::kOamAddr, oa + 1);
+        } else if (r == 5) {
+            const std::uint32_t t = r16(reg::kT);
+            if (!r8(reg::kW)) {
+                w8(reg::kFineX, val & 7);
+                w16(reg::kT, (t & 0xFFE0) | (val >> 3));
+                w8(reg::kScrollX, val);
+                w8(reg::kW, 1);
+            } else {
+                w16(reg::kT, (((t & 0x8FFF) | ((val & 0x07) << 12)) & 0xFC1F) | ((val & 0xF8) << 2));
+                w8(reg::kScrollY, val);
+                w8(reg::kW, 0);
+            }
+        } else if (r == 6) {
+            const std::uint32_t t = r16(reg::kT);
+            if (!r8(reg::kW)) {
+                w16(reg::kT, (t & 0x00FF) | ((val & 0x3F) << 8));
+                w8(reg::kW, 1);
+            } else {
+                const std::uint32_t nt = (t & 0x7F00) | val;
+                w16(reg::kT, nt);
+                w16(reg::kV, nt);
+                w8(reg::kW, 0);
+            }
+        } else if (r == 7) {
+            const std::uint32_t v = r16(reg::kV);
+            vram_wr(v, val);
+            w16(reg::kV, v + ((r8(reg::kCtrl) & 0x04) ? 32u : 1u));
         }
     }
 
@@ -287,12 +310,12 @@ struct Console {
         }
         if (addr == 0x4016) {
             const std::uint32_t next = val & 1;
-            if (next || strobe) {
-                c1_shift = c1_buttons;
-                c1_count = 0;
-                c2_count = 0;
+            if (next || r8(reg::kStrobe)) {
+                w8(reg::kC1Shift, r8(reg::kC1Buttons));
+                w8(reg::kC1Count, 0);
+                w8(reg::kC2Count, 0);
             }
-            strobe = next;
+            w8(reg::kStrobe, next);
         }
         return 0;
     }
@@ -308,9 +331,11 @@ struct Console {
     // ---- PPU timing (ppu.hpp:46-76) -------------------------------------------------
     // Advance by `dots` (less than one frame past the next frame end), applying
     // every event crossed in order.  Returns frames completed (0 or 1).
-    __device__ __forceinline__ std::uint32_t settle(std::uint32_t dots) {
-        const std::uint32_t start = frame_dot, end = start + dots;
+    __device__ std::uint32_t settle(std::uint32_t dots) {
+        const std::uint32_t start = r32(reg::kFrameDot), end = start + dots;
         const std::uint32_t fc = end >= kFrameDots ? 1u : 0u;
+        std::uint32_t status = r8(reg::kStatus);
+        const std::uint32_t mask = r8(reg::kMask), ctrl = r8(reg::kCtrl);
         for (std::uint32_t fo = 0; fo <= fc; ++fo) {
             const std::uint32_t off = fo * kFrameDots;
             auto crossed = [&](std::uint32_t ev) { return start < off + ev && off + ev <= end; };
@@ -324,7 +349,8 @@ struct Console {
                 nmi = 0;
             }
         }
-        frame_dot = end - fc * kFrameDots;
+        w8(reg::kStatus, status);
+        w32(reg::kFrameDot, end - fc * kFrameDots);
         return fc;
     }
 };
@@ -353,7 +379,10 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
     }
     const std::uint32_t base = kLdsRam + (lane < L ? slot : 0u) * C::kStride;
     const std::uint32_t P = s.pitch;
-    if (mine) {  // this console's RAM rows that live in LDS
+    C c{s, mine ? env : 0u, base, P};
+    std::uint32_t frames_left = 0;
+    if (mine) {
+        // This console's RAM rows that live in LDS.
         const std::uint8_t* g = s.ram + env;
         auto stage = [&](std::uint32_t ra, std::uint32_t at) {
             const std::size_t r = ra;
@@ -366,41 +395,34 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
             for (std::uint32_t ra = 0; ra < 0x100; ra += 4) stage(ra, ra);
             for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, ra - 0x80);
         }
-    }
-    __syncthreads();
-
-    C c{s, mine ? env : 0u, base, P};
-    c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
-    c.brk_vec = lds[0x7FFE] | (lds[0x7FFF] << 8);
-    std::uint32_t frames_left = 0, fd0 = 0;
-    if (mine) {
+        // PPU and pad registers.
+        c.w8(reg::kCtrl, s.ctrl[env]); c.w8(reg::kMask, s.mask[env]); c.w8(reg::kStatus, s.status[env]);
+        c.w8(reg::kOamAddr, s.oam_addr[env]); c.w8(reg::kOpenBus, s.open_bus[env]);
+        c.w8(reg::kReadBuffer, s.read_buffer[env]); c.w8(reg::kFineX, s.fine_x[env]); c.w8(reg::kW, s.w[env]);
+        c.w8(reg::kScrollX, s.scroll_x[env]); c.w8(reg::kScrollY, s.scroll_y[env]);
+        c.w16(reg::kV, s.v[env]); c.w16(reg::kT, s.t[env]); c.w32(reg::kFrameDot, s.frame_dot[env]);
+        // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
+        const std::uint32_t buttons = s.actions[env], strobe = s.strobe[env];
+        c.w8(reg::kC1Buttons, buttons);
+        c.w8(reg::kC1Shift, strobe ? buttons : s.c1_shift[env]);
+        c.w8(reg::kC1Count, strobe ? 0u : s.c1_count[env]);
+        c.w8(reg::kStrobe, strobe);
+        c.w8(reg::kC2Count, s.c2_count[env]);
         c.pc = s.pc[env];
         c.regs = s.a[env] | (s.x[env] << 8) | (s.y[env] << 16) | (static_cast<std::uint32_t>(s.sp[env]) << 24);
         c.p = s.p[env];
-        c.frame_dot = s.frame_dot[env]; c.status = s.status[env]; c.ctrl = s.ctrl[env]; c.mask = s.mask[env];
         c.nmi = s.nmi_pending[env];
-        c.oam_addr = s.oam_addr[env]; c.open_bus = s.open_bus[env]; c.read_buffer = s.read_buffer[env];
-        c.v = s.v[env]; c.t = s.t[env]; c.fine_x = s.fine_x[env]; c.w = s.w[env];
-        c.scroll_x = s.scroll_x[env]; c.scroll_y = s.scroll_y[env];
-        // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
-        c.c1_buttons = s.actions[env];
-        c.c1_shift = s.c1_shift[env]; c.c1_count = s.c1_count[env]; c.strobe = s.strobe[env];
-        c.c2_count = s.c2_count[env];
-        if (c.strobe) {
-            c.c1_shift = c.c1_buttons;
-            c.c1_count = 0;
-        }
         c.fault = s.fault[env];
         frames_left = c.fault ? 0u : frameskip;
     } else {
-        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.frame_dot = 0; c.status = 0; c.ctrl = 0; c.mask = 0; c.nmi = 0;
-        c.oam_addr = 0; c.open_bus = 0; c.read_buffer = 0; c.v = 0; c.t = 0; c.fine_x = 0; c.w = 0;
-        c.scroll_x = 0; c.scroll_y = 0; c.c1_buttons = 0; c.c1_shift = 0; c.c1_count = 0; c.strobe = 0;
-        c.c2_count = 0; c.fault = 0;
+        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.nmi = 0; c.fault = 0;
     }
     c.dma = 0;
-    fd0 = c.frame_dot;
-    std::uint32_t horizon = to_event(c.frame_dot);
+    __syncthreads();
+    c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
+    c.brk_vec = lds[0x7FFE] | (lds[0x7FFF] << 8);
+    const std::uint32_t fd0 = mine ? c.r32(reg::kFrameDot) : 0u;
+    std::uint32_t horizon = to_event(fd0);
     std::int32_t left = static_cast<std::int32_t>(horizon);
     std::uint32_t frames = 0, in_frame = 0, budget_hits = 0;
     std::uint64_t instructions = 0;
@@ -433,145 +455,175 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
             const uint4 m = reinterpret_cast<const uint4*>(lds + kLdsMicro)[op];
             const std::uint32_t d0 = m.x, d1 = m.y, d2 = m.z, d3 = m.w;
             const std::uint32_t kind = (d0 >> 10) & 3;
-            if (kind == mc::KILLEGAL) {
+            // Every conditional below selects between values that are already
+            // computed, so the compiler emits v_cndmask instead of divergent
+            // branches; only memory side paths branch.
+            // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
+            const std::uint32_t xreg = ubfe(c.regs, 8, 8);
+            const std::uint32_t pidx = ((op & 0x1F) == 0x01) ? xreg : 0u;
+            const std::uint32_t pz = (b1 + pidx) & 0xFF;
+            const std::uint32_t pz1 = (pz + 1) & 0xFF;
+            const std::uint32_t ptr = lds[base + pz] | (lds[base + pz1] << 8);
+            // Effective address.
+            const std::uint32_t abs = b1 | (b2 << 8);
+            const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
+            const std::uint32_t idx = ubfe(c.regs, d0, d1);
+            const std::uint32_t ea_full = ebase + idx;
+            const std::uint32_t ea_mask = (d0 & 0x40) ? 0xFFu : 0xFFFFu;
+            const std::uint32_t ea = ea_full & ea_mask;
+            const std::uint32_t cross = (((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1;
+            dots += ((d0 >> 14) & 31) + 3 * cross;
+            // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
+            // rows, PRG RAM) or the I/O registers.
+            const std::uint32_t ra = ea & 0x7FF;
+            const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
+            const bool ram_lds = is_ram && C::ram_in_lds(ra);
+            const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
+            const bool io = !is_ram && ea < 0x6000;
+            const std::uint32_t rom_off = ea & 0x7FFF;
+            const std::uint32_t ram_off = base + C::ram_lds_off(ra);
+            const std::uint32_t spare = base + C::kSpare;
+            const std::uint32_t laddr0 = ram_lds ? ram_off : spare;
+            const std::uint32_t laddr = rom ? rom_off : laddr0;
+            const std::uint32_t prgram_row = ea - 0x5800;
+            const std::uint32_t row = is_ram ? ra : prgram_row;
+            const bool rd = d0 & 0x100;
+            const bool wr = (d0 & 0x200) && kind != mc::KILLEGAL;
+            const std::uint32_t ml = lds[laddr];
+            std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
+            if (rd && glob) M = s.ram[c.goff(row)];
+            if (rd && io) M = c.io_rd(ea);
+            // Adder, logic unit and right shifter.
+            const std::uint32_t R = ubfe(c.regs, d2, 8);
+            const std::uint32_t xa = (d1 & 0x20) ? M : R;
+            const std::uint32_t bsrc = (d1 & 0x40) ? xa : M;
+            const std::uint32_t xb = (bsrc & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
+            const std::uint32_t cf = c.p & 1;
+            const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
+            const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
+            const bool right = d1 & 0x200;
+            const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
+            const std::uint32_t ar = (sum & (d2 >> 24)) | lres;
+            const std::uint32_t r = right ? sr : ar;
+            const std::uint32_t c_right = xa & 1, c_add = (sum >> 8) & 1;
+            const std::uint32_t carry = right ? c_right : c_add;
+            const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
+            const std::uint32_t nv_bit = M & 0xC0, nv_alu = (r & 0x80) | ovf;
+            const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
+            const std::uint32_t f = nv | (r == 0 ? 2u : 0u) | carry;
+            const std::uint32_t fm = d0 >> 24;
+            const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
+            c.p = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
+            // Register write-back.
+            const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
+            c.regs = (c.regs & ~dmask) | ((r << doff) & dmask);
+            // Memory write: LDS RAM (non-writers store to their spare byte),
+            // HBM, or an I/O register.
+            const std::uint32_t waddr = (wr && ram_lds) ? laddr : spare;
+            lds[waddr] = static_cast<std::uint8_t>(r);
+            if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
+            if (wr && io) dots += c.io_wr(ea, r);
+            // Next PC: fall through or branch.
+            const std::uint32_t fall = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
+            const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
+            const std::uint32_t target = (fall + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
+            const std::uint32_t bdots = ((fall ^ target) & 0xFF00) ? 6u : 3u;
+            const std::uint32_t tdots = taken ? bdots : 0u;
+            dots += tdots;
+            std::uint32_t next = taken ? target : fall;
+            if (kind == mc::KCTRL) {
+                // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
+                // JSR/BRK/PHA/PHP push, RTS/RTI/PLA/PLP pull.
+                const std::uint32_t op_c = (d0 >> 19) & 15;
+                constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
+                                                  (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
+                constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
+                                                 (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
+                const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
+                const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
+                const std::uint32_t sp = c.regs >> 24;
+                const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
+                const std::uint32_t pb = c.p | 0x30;
+                const std::uint32_t areg = c.regs & 0xFF, rethi = ret >> 8, retlo = ret & 0xFF;
+                const std::uint32_t v0a = op_c == mc::PHP ? pb : rethi;
+                const std::uint32_t v0 = op_c == mc::PHA ? areg : v0a;
+                if (npush >= 1) c.ram_wr(0x100 | sp, v0);
+                if (npush >= 2) c.ram_wr(0x100 | ((sp - 1) & 0xFF), retlo);
+                if (npush >= 3) c.ram_wr(0x100 | ((sp - 2) & 0xFF), pb);
+                std::uint32_t w0 = 0, w1 = 0, w2 = 0;
+                if (npull >= 1) w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
+                if (npull >= 2) w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
+                if (npull >= 3) w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
+                const std::uint32_t nsp = (sp - npush + npull) & 0xFF;
+                c.regs = (c.regs & 0x00FFFFFFu) | (nsp << 24);
+                const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
+                const std::uint32_t brk_p = c.p | 0x24;
+                const std::uint32_t p_b = op_c == mc::BRK ? brk_p : c.p;
+                c.p = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : p_b;
+                if (op_c == mc::PLA) {
+                    c.regs = (c.regs & ~0xFFu) | w0;
+                    c.p = (c.p & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
+                }
+                const std::uint32_t rts_pc = ((w0 | (w1 << 8)) + 1) & 0xFFFF, rti_pc = w1 | (w2 << 8);
+                const std::uint32_t n3 = op_c == mc::BRK ? c.brk_vec : next;
+                const std::uint32_t n2 = op_c == mc::RTI ? rti_pc : n3;
+                const std::uint32_t n1 = op_c == mc::RTS ? rts_pc : n2;
+                next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs : n1;
+                if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
+                    const std::uint32_t l = c.bus_rd(abs);
+                    next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
+                }
+                // Idle loop (JMP to itself): the console repeats 3-cycle jumps
+                // until the next timing event; account for them in one go.
+                const std::int32_t gap = left - static_cast<std::int32_t>(dots);
+                if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
+                    std::int32_t k = (gap + 8) / 9;
+                    if (kBudget) {
+                        const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
+                        k = k < room ? k : room;
+                    }
+                    dots += 9u * static_cast<std::uint32_t>(k);
+                    in_frame += static_cast<std::uint32_t>(k);
+                    instructions += static_cast<std::uint64_t>(k);
+                    if constexpr (kStats == 2) {
+                        atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
+                        atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
+                    }
+                }
+            }
+            if (kind == mc::KILLEGAL) {  // the console freezes before executing it
                 c.fault |= 1;
                 active = false;
-            } else {
-                // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
-                const std::uint32_t pz = (b1 + (((op & 0x1F) == 0x01) ? ubfe(c.regs, 8, 8) : 0u)) & 0xFF;
-                const std::uint32_t ptr = lds[base + pz] | (lds[base + ((pz + 1) & 0xFF)] << 8);
-                // Effective address.
-                const std::uint32_t abs = b1 | (b2 << 8);
-                const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
-                const std::uint32_t idx = ubfe(c.regs, d0, d1);
-                const std::uint32_t ea = (ebase + idx) & ((d0 & 0x40) ? 0xFFu : 0xFFFFu);
-                dots += ((d0 >> 14) & 31) + 3 * ((((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1);
-                // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
-                // rows, PRG RAM) or the I/O registers.
-                const std::uint32_t ra = ea & 0x7FF;
-                const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
-                const bool ram_lds = is_ram && C::ram_in_lds(ra);
-                const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
-                const bool io = !is_ram && ea < 0x6000;
-                const std::uint32_t laddr = rom ? (ea & 0x7FFF) : (ram_lds ? base + C::ram_lds_off(ra) : base + C::kSpare);
-                const std::uint32_t row = is_ram ? ra : ea - 0x5800;
-                const bool rd = d0 & 0x100, wr = d0 & 0x200;
-                const std::uint32_t ml = lds[laddr];
-                std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
-                if (rd && glob) M = s.ram[c.goff(row)];
-                if (rd && io) M = c.io_rd(ea);
-                // Adder, logic unit and right shifter.
-                const std::uint32_t R = ubfe(c.regs, d2, 8);
-                const std::uint32_t xa = (d1 & 0x20) ? M : R;
-                const std::uint32_t xb = (((d1 & 0x40) ? xa : M) & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
-                const std::uint32_t cf = c.p & 1;
-                const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
-                const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
-                const bool right = d1 & 0x200;
-                const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
-                const std::uint32_t r = right ? sr : ((sum & (d2 >> 24)) | lres);
-                const std::uint32_t carry = right ? (xa & 1) : ((sum >> 8) & 1);
-                const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
-                const std::uint32_t nv = (d0 & 0x800000) ? (M & 0xC0) : ((r & 0x80) | ovf);
-                const std::uint32_t f = nv | ((r & 0xFF) == 0 ? 2u : 0u) | carry;
-                const std::uint32_t fm = d0 >> 24;
-                const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
-                c.p = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
-                // Register write-back.
-                const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
-                c.regs = (c.regs & ~dmask) | ((r << doff) & dmask);
-                // Memory write: LDS RAM (non-writers store to their spare byte),
-                // HBM, or an I/O register.
-                lds[(wr && ram_lds) ? laddr : base + C::kSpare] = static_cast<std::uint8_t>(r);
-                if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
-                if (wr && io) dots += c.io_wr(ea, r & 0xFF);
-                // Next PC: fall through or branch.
-                std::uint32_t next = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
-                const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
-                const std::uint32_t target = (next + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
-                dots += taken ? (((next ^ target) & 0xFF00) ? 6u : 3u) : 0u;
-                next = taken ? target : next;
-                if (kind == mc::KCTRL) {
-                    // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
-                    // JSR/BRK/PHA/PHP push, RTS/RTI/PLA/PLP pull.
-                    const std::uint32_t op_c = (d0 >> 19) & 15;
-                    constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
-                                                      (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
-                    constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
-                                                     (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
-                    const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
-                    const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
-                    const std::uint32_t sp = c.regs >> 24;
-                    const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
-                    const std::uint32_t pb = c.p | 0x30;
-                    const std::uint32_t v0 = op_c == mc::PHA ? (c.regs & 0xFF) : (op_c == mc::PHP ? pb : (ret >> 8));
-                    if (npush >= 1) c.ram_wr(0x100 | sp, v0);
-                    if (npush >= 2) c.ram_wr(0x100 | ((sp - 1) & 0xFF), ret & 0xFF);
-                    if (npush >= 3) c.ram_wr(0x100 | ((sp - 2) & 0xFF), pb);
-                    std::uint32_t w0 = 0, w1 = 0, w2 = 0;
-                    if (npull >= 1) w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
-                    if (npull >= 2) w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
-                    if (npull >= 3) w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
-                    c.regs = (c.regs & 0x00FFFFFFu) | (((sp - npush + npull) & 0xFF) << 24);
-                    const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
-                    c.p = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : (op_c == mc::BRK ? (c.p | 0x24) : c.p);
-                    if (op_c == mc::PLA) {
-                        c.regs = (c.regs & ~0xFFu) | w0;
-                        c.p = (c.p & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
-                    }
-                    next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs
-                         : op_c == mc::RTS ? ((w0 | (w1 << 8)) + 1) & 0xFFFF
-                         : op_c == mc::RTI ? (w1 | (w2 << 8))
-                         : op_c == mc::BRK ? c.brk_vec : next;
-                    if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
-                        const std::uint32_t l = c.bus_rd(abs);
-                        next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
-                    }
-                    // Idle loop (JMP to itself): the console repeats 3-cycle jumps
-                    // until the next timing event; account for them in one go.
-                    const std::int32_t gap = left - static_cast<std::int32_t>(dots);
-                    if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
-                        std::int32_t k = (gap + 8) / 9;
-                        if (kBudget) {
-                            const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
-                            k = k < room ? k : room;
-                        }
-                        dots += 9u * static_cast<std::uint32_t>(k);
-                        in_frame += static_cast<std::uint32_t>(k);
-                        instructions += static_cast<std::uint64_t>(k);
-                        if constexpr (kStats == 2) {
-                            atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
-                            atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
-                        }
-                    }
-                }
-                c.pc = next;
-                if constexpr (kStats == 2) {
-                    atomicAdd(&s.prof_opcodes[op], 1ull);
-                    atomicAdd(&s.prof_pcs[pc0], 1ull);
-                }
-                ++in_frame;
-                ++instructions;
-                left -= static_cast<std::int32_t>(dots);
-                if (left <= 0) {  // a timing event was crossed: settle the PPU
-                    const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
-                    horizon = to_event(c.frame_dot);
-                    left = static_cast<std::int32_t>(horizon);
-                    if (fc) {
-                        ++frames;
-                        in_frame = 0;
-                        if (--frames_left == 0) active = false;
-                    }
-                }
-                if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
-                    const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
-                    horizon = to_event(c.frame_dot);
-                    left = static_cast<std::int32_t>(horizon);
-                    frames += fc;
-                    budget_hits += fc ? 0u : 1u;
+                next = pc0;
+                dots = 0;
+            }
+            c.pc = next;
+            if constexpr (kStats == 2) {
+                atomicAdd(&s.prof_opcodes[op], 1ull);
+                atomicAdd(&s.prof_pcs[pc0], 1ull);
+            }
+            const std::uint32_t counted = kind != mc::KILLEGAL ? 1u : 0u;  // a fault is not an instruction
+            in_frame += counted;
+            instructions += counted;
+            left -= static_cast<std::int32_t>(dots);
+            if (left <= 0) {  // a timing event was crossed: settle the PPU
+                const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
+                horizon = to_event(c.r32(reg::kFrameDot));
+                left = static_cast<std::int32_t>(horizon);
+                if (fc) {
+                    ++frames;
                     in_frame = 0;
                     if (--frames_left == 0) active = false;
                 }
+            }
+            if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
+                const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
+                horizon = to_event(c.r32(reg::kFrameDot));
+                left = static_cast<std::int32_t>(horizon);
+                frames += fc;
+                budget_hits += fc ? 0u : 1u;
+                in_frame = 0;
+                if (--frames_left == 0) active = false;
             }
         }
         // OAM DMA ($4014, console.hpp:191-197): the whole wave copies one
@@ -583,9 +635,9 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
             const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(req)) - 1);
             req &= req - 1;
             const std::uint32_t page = __builtin_amdgcn_readlane(c.dma, src) & 0xFF;
-            const std::uint32_t oa = __builtin_amdgcn_readlane(c.oam_addr, src);
             const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
             const std::uint32_t e_base = __builtin_amdgcn_readlane(c.base, src);
+            const std::uint32_t oa = lds[e_base + C::kRegs + reg::kOamAddr];
             if (page < 0x20 || page >= 0x60) {
                 for (std::uint32_t k = 0; k < 4; ++k) {
                     const std::uint32_t i = 4 * lane + k;
@@ -593,23 +645,24 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
                     std::uint32_t val;
                     if (page < 0x20) {
                         const std::uint32_t ra = addr & 0x7FF;
-                        val = C::ram_in_lds(ra) ? lds[e_base + C::ram_lds_off(ra)] : s.ram[ra * P + e_env];
+                        val = C::ram_in_lds(ra) ? lds[e_base + C::ram_lds_off(ra)] : s.ram[__umul24(ra, P) + e_env];
                     } else if (page < 0x80) {
-                        val = s.ram[(addr - 0x5800) * P + e_env];
+                        val = s.ram[__umul24(addr - 0x5800, P) + e_env];
                     } else {
                         val = lds[addr & 0x7FFF];
                     }
-                    s.oam[((oa + i) & 0xFF) * P + e_env] = static_cast<std::uint8_t>(val);
+                    s.oam[__umul24((oa + i) & 0xFF, P) + e_env] = static_cast<std::uint8_t>(val);
                 }
             } else if (lane == src) {
                 // OAMADDR advances with every byte (ppu.hpp:131-134), which a
                 // $2004 read inside the copy observes; it wraps back to `oa`.
                 for (std::uint32_t i = 0; i < 256; ++i) {
-                    c.oam_addr = (oa + i) & 0xFF;
+                    const std::uint32_t at = (oa + i) & 0xFF;
+                    c.w8(reg::kOamAddr, at);
                     const std::uint32_t val = c.bus_rd((page << 8) | i);
-                    s.oam[c.oam_addr * P + e_env] = static_cast<std::uint8_t>(val);
+                    s.oam[__umul24(at, P) + e_env] = static_cast<std::uint8_t>(val);
                 }
-                c.oam_addr = oa;
+                c.w8(reg::kOamAddr, oa);
             }
         }
         c.dma = 0;
@@ -618,7 +671,7 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
     if (!mine) return;
     if (left != static_cast<std::int32_t>(horizon)) frames += c.settle(horizon - static_cast<std::uint32_t>(left));
 
-    // Write the LDS-resident RAM rows back to HBM.
+    // Write the LDS-resident RAM rows and registers back to HBM.
     {
         std::uint8_t* g = s.ram + env;
         auto unstage = [&](std::uint32_t ra, std::uint32_t at) {
@@ -636,7 +689,7 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
             for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) unstage(ra, ra - 0x80);
         }
     }
-
+    const std::uint32_t fd = c.r32(reg::kFrameDot);
     s.pc[env] = static_cast<std::uint16_t>(c.pc);
     s.a[env] = static_cast<std::uint8_t>(c.regs);
     s.x[env] = static_cast<std::uint8_t>(c.regs >> 8);
@@ -644,20 +697,28 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
     s.sp[env] = static_cast<std::uint8_t>(c.regs >> 24);
     s.p[env] = static_cast<std::uint8_t>(c.p);
     // Every CPU cycle is 3 PPU dots.
-    const std::uint64_t advanced = static_cast<std::uint64_t>(frames) * kFrameDots + c.frame_dot - fd0;
+    const std::uint64_t advanced = static_cast<std::uint64_t>(frames) * kFrameDots + fd - fd0;
     s.cycles[env] += advanced / 3;
     s.frame[env] += frames;
-    s.frame_dot[env] = c.frame_dot;
-    s.status[env] = static_cast<std::uint8_t>(c.status); s.ctrl[env] = static_cast<std::uint8_t>(c.ctrl);
-    s.mask[env] = static_cast<std::uint8_t>(c.mask); s.nmi_pending[env] = static_cast<std::uint8_t>(c.nmi);
-    s.oam_addr[env] = static_cast<std::uint8_t>(c.oam_addr); s.open_bus[env] = static_cast<std::uint8_t>(c.open_bus);
-    s.read_buffer[env] = static_cast<std::uint8_t>(c.read_buffer);
-    s.v[env] = static_cast<std::uint16_t>(c.v); s.t[env] = static_cast<std::uint16_t>(c.t);
-    s.fine_x[env] = static_cast<std::uint8_t>(c.fine_x); s.w[env] = static_cast<std::uint8_t>(c.w);
-    s.scroll_x[env] = static_cast<std::uint8_t>(c.scroll_x); s.scroll_y[env] = static_cast<std::uint8_t>(c.scroll_y);
-    s.c1_buttons[env] = static_cast<std::uint8_t>(c.c1_buttons); s.c1_shift[env] = static_cast<std::uint8_t>(c.c1_shift);
-    s.c1_count[env] = static_cast<std::uint8_t>(c.c1_count); s.strobe[env] = static_cast<std::uint8_t>(c.strobe);
-    s.c2_count[env] = static_cast<std::uint8_t>(c.c2_count);
+    s.frame_dot[env] = fd;
+    s.nmi_pending[env] = static_cast<std::uint8_t>(c.nmi);
+    s.status[env] = static_cast<std::uint8_t>(c.r8(reg::kStatus));
+    s.ctrl[env] = static_cast<std::uint8_t>(c.r8(reg::kCtrl));
+    s.mask[env] = static_cast<std::uint8_t>(c.r8(reg::kMask));
+    s.oam_addr[env] = static_cast<std::uint8_t>(c.r8(reg::kOamAddr));
+    s.open_bus[env] = static_cast<std::uint8_t>(c.r8(reg::kOpenBus));
+    s.read_buffer[env] = static_cast<std::uint8_t>(c.r8(reg::kReadBuffer));
+    s.v[env] = static_cast<std::uint16_t>(c.r16(reg::kV));
+    s.t[env] = static_cast<std::uint16_t>(c.r16(reg::kT));
+    s.fine_x[env] = static_cast<std::uint8_t>(c.r8(reg::kFineX));
+    s.w[env] = static_cast<std::uint8_t>(c.r8(reg::kW));
+    s.scroll_x[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollX));
+    s.scroll_y[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollY));
+    s.c1_buttons[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Buttons));
+    s.c1_shift[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Shift));
+    s.c1_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Count));
+    s.strobe[env] = static_cast<std::uint8_t>(c.r8(reg::kStrobe));
+    s.c2_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC2Count));
     s.fault[env] = static_cast<std::uint8_t>(c.fault);
 
     float reward = 0.0f;
