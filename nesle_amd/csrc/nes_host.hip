@@ -261,7 +261,8 @@ struct nesle_batch {
         add(&ds.apu_io, nesle::kApuIoBytes * P);
         // RAM rows 0-2047 and PRG RAM rows 2048-10239 form one interleaved array,
         // so the step kernel reaches both with one row * pitch + env offset.
-        add(&ds.ram, static_cast<std::size_t>(nesle::kRamBytes + nesle::kPrgRamBytes) * P);
+        // Plus one spare row that the step kernel's lanes with nothing to store write to.
+        add(&ds.ram, static_cast<std::size_t>(nesle::kRamBytes + nesle::kPrgRamBytes + 1) * P);
         add(&ds.oam, nesle::kOamBytes * P);
         add(&ds.palette, nesle::kPaletteBytes * P);
         add(&ds.nametable, static_cast<std::size_t>(ds.nt_bytes) * P);

@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "nes_device.h"
 #include "nes_launch.h"
@@ -58,19 +59,29 @@ __constant__ uint4 c_micro[256] = {
 
 extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 
-constexpr std::uint32_t kBlock = 256;           // 4 waves
+constexpr std::uint32_t kMaxBlock = 1024;       // up to 16 waves per workgroup
 constexpr std::uint32_t kLdsMicro = 32768;      // 256 x 16 B
 constexpr std::uint32_t kLdsRam = 32768 + 4096; // console RAM blocks
-// Per-console LDS block: RAM rows, 4 spare bytes, then the PPU/pad registers.
-constexpr std::uint32_t kSplitStride = 412;     // $0000-$00FF, $0180-$01FF, spare, registers
-constexpr std::uint32_t kFullStride = 2076;     // $0000-$07FF, spare, registers
+// Per-console LDS block: RAM rows, 4 spare bytes, then a 40-byte register
+// area (PPU/pad registers and the rarely touched loop state).  Strides are an
+// odd number of dwords, so lanes at equal offsets hit distinct banks.
+constexpr std::uint32_t kSplitStride = 428;     // $0000-$00FF, $0180-$01FF, spare, registers
+constexpr std::uint32_t kFullStride = 2092;     // $0000-$07FF, spare, registers
 // Register area offsets (bytes from the start of the area).
 namespace reg {
 constexpr std::uint32_t kCtrl = 0, kMask = 1, kStatus = 2, kOamAddr = 3, kOpenBus = 4, kReadBuffer = 5;
 constexpr std::uint32_t kFineX = 6, kW = 7, kScrollX = 8, kScrollY = 9, kC1Buttons = 10, kC1Shift = 11;
-constexpr std::uint32_t kC1Count = 12, kStrobe = 13, kC2Count = 14, kV = 16, kT = 18, kFrameDot = 20;
-constexpr std::uint32_t kBytes = 24;
+constexpr std::uint32_t kC1Count = 12, kStrobe = 13, kC2Count = 14, kDmaPage = 15, kV = 16, kT = 18;
+constexpr std::uint32_t kFrameDot = 20, kHorizon = 24, kFramesLeft = 28, kFrames = 32, kBudgetHits = 36;
+constexpr std::uint32_t kBytes = 40;
 }  // namespace reg
+
+// Bits of a console's `flags` VGPR.
+constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4;
+
+// Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
+// write to (one spare byte per console after PRG RAM).
+constexpr std::uint32_t kTrashRow = kRamBytes + kPrgRamBytes;
 constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 
 constexpr std::uint32_t lds_bytes(std::uint32_t consoles, bool full) {
@@ -112,11 +123,10 @@ struct Console {
     const DeviceState& s;
     std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
-    // Hot state in VGPRs: CPU registers, the NMI latch, a pending OAM DMA
-    // (page | 0x100) and the fault flag.  PPU and pad registers live in the
-    // console's LDS register area (reg::*): only the I/O paths, PPU settlement
-    // and NMI entry touch them.
-    std::uint32_t pc, regs, p, nmi, dma, fault;
+    // Hot state in VGPRs: CPU registers and `flags` (NMI latch, pending OAM
+    // DMA, fault).  PPU and pad registers live in the console's LDS register
+    // area (reg::*): only the I/O paths, PPU settlement and NMI entry touch them.
+    std::uint32_t pc, regs, p, flags;
 
     // ---- LDS register area ----------------------------------------------------------
     __device__ __forceinline__ std::uint32_t r8(std::uint32_t f) const { return lds[base + kRegs + f]; }
@@ -203,7 +213,7 @@ struct Console {
                 const std::uint32_t st = r8(reg::kStatus);
                 const std::uint32_t val = (st & 0xE0) | (r8(reg::kOpenBus) & 0x1F);
                 w8(reg::kStatus, st & 0x7F);
-                nmi = 0;
+                flags &= ~kNmiPending;
                 w8(reg::kW, 0);
                 w8(reg::kOpenBus, val);
                 return val;
@@ -255,7 +265,7 @@ struct Console {
         w8(reg::kOpenBus, val);
         if (r == 0) {
             const std::uint32_t ctrl = r8(reg::kCtrl);
-            if ((val & 0x80) && !(ctrl & 0x80) && (r8(reg::kStatus) & 0x80)) nmi = 1;
+            if ((val & 0x80) && !(ctrl & 0x80) && (r8(reg::kStatus) & 0x80)) flags |= kNmiPending;
             w8(reg::kCtrl, val);
             w16(reg::kT, (r16(reg::kT) & 0xF3FF) | ((val & 0x03) << 10));
         } else if (r == 1) {
@@ -304,8 +314,9 @@ struct Console {
         }
         if (addr >= 0x4018) return 0;
         s.apu_io[goff(addr - 0x4000)] = static_cast<std::uint8_t>(val);
-        if (addr == 0x4014) {
-            dma = 0x100 | val;  // copied by the wave right after this instruction
+        if (addr == 0x4014) {  // copied by the wave right after this instruction
+            w8(reg::kDmaPage, val);
+            flags |= kDmaPending;
             return 3 * 513;
         }
         if (addr == 0x4016) {
@@ -341,12 +352,12 @@ struct Console {
             auto crossed = [&](std::uint32_t ev) { return start < off + ev && off + ev <= end; };
             if (crossed(kSprite0Dot) && (mask & 0x18)) status |= 0x40;
             if (crossed(kVblankDot)) {
-                if (!(status & 0x80) && (ctrl & 0x80)) nmi = 1;
+                if (!(status & 0x80) && (ctrl & 0x80)) flags |= kNmiPending;
                 status |= 0x80;
             }
             if (crossed(kPreRenderDot)) {
                 status &= 0x1F;
-                nmi = 0;
+                flags &= ~kNmiPending;
             }
         }
         w8(reg::kStatus, status);
@@ -361,26 +372,26 @@ struct Console {
 // bind (a frame always completes within 14,891 instructions, since every
 // instruction advances the PPU by at least 6 dots).
 template <int kStats, bool kFull, bool kBudget>
-__global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32_t frameskip, std::uint32_t max_instr,
-                                                      std::uint32_t auto_reset, std::uint32_t lane_bits) {
+__global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uint32_t frameskip, std::uint32_t max_instr,
+                                                         std::uint32_t auto_reset, std::uint32_t lane_bits) {
     using C = Console<kFull>;
-    const std::uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const std::uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, T = blockDim.x;
     const std::uint32_t L = 1u << lane_bits;
     const std::uint32_t slot = wave * L + lane;
-    const std::uint32_t env = xcd_block(blockIdx.x, gridDim.x) * (4u * L) + slot;
+    const std::uint32_t env = xcd_block(blockIdx.x, gridDim.x) * ((T >> 6) * L) + slot;
     const bool mine = lane < L && env < s.n;
 
     {   // PRG ROM (a 16 KB image mirrored to 32 KB) and the microcode table.
         const std::uint32_t words = (s.prg_mask + 1) / 16;
         const uint4* src = reinterpret_cast<const uint4*>(s.prg_rom);
         uint4* dst = reinterpret_cast<uint4*>(lds);
-        for (std::uint32_t i = tid; i < kPrgRomMax / 16; i += kBlock) dst[i] = src[i & (words - 1)];
-        reinterpret_cast<uint4*>(lds + kLdsMicro)[tid] = c_micro[tid];
+        for (std::uint32_t i = tid; i < kPrgRomMax / 16; i += T) dst[i] = src[i & (words - 1)];
+        if (tid < 256) reinterpret_cast<uint4*>(lds + kLdsMicro)[tid] = c_micro[tid];
     }
     const std::uint32_t base = kLdsRam + (lane < L ? slot : 0u) * C::kStride;
     const std::uint32_t P = s.pitch;
     C c{s, mine ? env : 0u, base, P};
-    std::uint32_t frames_left = 0;
+    std::uint32_t fd0 = 0, horizon0 = 0;
     if (mine) {
         // This console's RAM rows that live in LDS.
         const std::uint8_t* g = s.ram + env;
@@ -395,12 +406,16 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
             for (std::uint32_t ra = 0; ra < 0x100; ra += 4) stage(ra, ra);
             for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, ra - 0x80);
         }
-        // PPU and pad registers.
+        // PPU and pad registers, and the loop state kept off the hot path.
         c.w8(reg::kCtrl, s.ctrl[env]); c.w8(reg::kMask, s.mask[env]); c.w8(reg::kStatus, s.status[env]);
         c.w8(reg::kOamAddr, s.oam_addr[env]); c.w8(reg::kOpenBus, s.open_bus[env]);
         c.w8(reg::kReadBuffer, s.read_buffer[env]); c.w8(reg::kFineX, s.fine_x[env]); c.w8(reg::kW, s.w[env]);
         c.w8(reg::kScrollX, s.scroll_x[env]); c.w8(reg::kScrollY, s.scroll_y[env]);
-        c.w16(reg::kV, s.v[env]); c.w16(reg::kT, s.t[env]); c.w32(reg::kFrameDot, s.frame_dot[env]);
+        c.w16(reg::kV, s.v[env]); c.w16(reg::kT, s.t[env]);
+        fd0 = s.frame_dot[env];
+        horizon0 = to_event(fd0);
+        c.w32(reg::kFrameDot, fd0);
+        c.w32(reg::kHorizon, horizon0);
         // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
         const std::uint32_t buttons = s.actions[env], strobe = s.strobe[env];
         c.w8(reg::kC1Buttons, buttons);
@@ -411,28 +426,38 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
         c.pc = s.pc[env];
         c.regs = s.a[env] | (s.x[env] << 8) | (s.y[env] << 16) | (static_cast<std::uint32_t>(s.sp[env]) << 24);
         c.p = s.p[env];
-        c.nmi = s.nmi_pending[env];
-        c.fault = s.fault[env];
-        frames_left = c.fault ? 0u : frameskip;
+        c.flags = (s.nmi_pending[env] ? kNmiPending : 0u) | (s.fault[env] ? kFault : 0u);
+        c.w32(reg::kFramesLeft, (c.flags & kFault) ? 0u : frameskip);
+        c.w32(reg::kFrames, 0);
+        c.w32(reg::kBudgetHits, 0);
     } else {
-        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.nmi = 0; c.fault = 0;
+        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.flags = 0;
     }
-    c.dma = 0;
     __syncthreads();
     c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
     c.brk_vec = lds[0x7FFE] | (lds[0x7FFF] << 8);
-    const std::uint32_t fd0 = mine ? c.r32(reg::kFrameDot) : 0u;
-    std::uint32_t horizon = to_event(fd0);
-    std::int32_t left = static_cast<std::int32_t>(horizon);
-    std::uint32_t frames = 0, in_frame = 0, budget_hits = 0;
+    std::int32_t left = static_cast<std::int32_t>(horizon0);
+    std::uint32_t in_frame = 0;
     std::uint64_t instructions = 0;
-    bool active = frames_left != 0;
+    bool active = mine && !(c.flags & kFault) && frameskip != 0;
+    // LDS offset of stack byte $0100 + x (valid for x >= 0x80 in split mode).
+    const std::uint32_t stk = base + (kFull ? 0x100u : 0x80u);
+    const std::uint32_t spare = base + C::kSpare;
 
+    // Every lane runs the datapath each iteration; `active` gates what is
+    // committed (registers, memory writes, I/O, control transfer, timing), so
+    // the loop body has no divergent region around the datapath.
     while (__ballot(active) != 0) {
-        if (active) {
-            std::uint32_t dots = 0;
-            if (c.nmi) {  // NMI entry before the instruction (cpu.hpp:112-123, console.hpp:111-115)
-                c.nmi = 0;
+        std::uint32_t dots = 0;
+        // Fetch: opcode and two operand bytes from the PRG image in LDS.
+        std::uint32_t pc0 = c.pc;
+        std::uint32_t off = pc0 & 0x7FFF;
+        std::uint32_t op = lds[off], b1 = lds[off + 1], b2 = lds[off + 2];
+        // Rare: NMI entry before the instruction (cpu.hpp:112-123,
+        // console.hpp:111-115) and code outside PRG ROM (bus reads, in order).
+        if (active && ((c.flags & kNmiPending) || (pc0 - 0x8000u) > 0x7FFDu)) {
+            if (c.flags & kNmiPending) {
+                c.flags &= ~kNmiPending;
                 const std::uint32_t sp = c.regs >> 24;
                 c.ram_wr(0x100 | sp, c.pc >> 8);
                 c.ram_wr(0x100 | ((sp - 1) & 0xFF), c.pc & 0xFF);
@@ -442,210 +467,241 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
                 c.pc = c.nmi_vec;
                 dots = 21;
             }
-            // Fetch: opcode and two operand bytes from the PRG image in LDS.
-            const std::uint32_t pc0 = c.pc;
-            const std::uint32_t off = pc0 & 0x7FFF;
-            std::uint32_t op = lds[off], b1 = lds[off + 1], b2 = lds[off + 2];
-            if (pc0 < 0x8000u || pc0 > 0xFFFDu) {  // code outside PRG ROM: bus reads, in order
+            pc0 = c.pc;
+            off = pc0 & 0x7FFF;
+            if ((pc0 - 0x8000u) <= 0x7FFDu) {
+                op = lds[off]; b1 = lds[off + 1]; b2 = lds[off + 2];
+            } else {
                 op = c.bus_rd(pc0);
                 const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
                 b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
                 b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
             }
-            const uint4 m = reinterpret_cast<const uint4*>(lds + kLdsMicro)[op];
-            const std::uint32_t d0 = m.x, d1 = m.y, d2 = m.z, d3 = m.w;
-            const std::uint32_t kind = (d0 >> 10) & 3;
-            // Every conditional below selects between values that are already
-            // computed, so the compiler emits v_cndmask instead of divergent
-            // branches; only memory side paths branch.
-            // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
-            const std::uint32_t xreg = ubfe(c.regs, 8, 8);
-            const std::uint32_t pidx = ((op & 0x1F) == 0x01) ? xreg : 0u;
-            const std::uint32_t pz = (b1 + pidx) & 0xFF;
-            const std::uint32_t pz1 = (pz + 1) & 0xFF;
-            const std::uint32_t ptr = lds[base + pz] | (lds[base + pz1] << 8);
-            // Effective address.
-            const std::uint32_t abs = b1 | (b2 << 8);
-            const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
-            const std::uint32_t idx = ubfe(c.regs, d0, d1);
-            const std::uint32_t ea_full = ebase + idx;
-            const std::uint32_t ea_mask = (d0 & 0x40) ? 0xFFu : 0xFFFFu;
-            const std::uint32_t ea = ea_full & ea_mask;
-            const std::uint32_t cross = (((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1;
-            dots += ((d0 >> 14) & 31) + 3 * cross;
-            // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
-            // rows, PRG RAM) or the I/O registers.
-            const std::uint32_t ra = ea & 0x7FF;
-            const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
-            const bool ram_lds = is_ram && C::ram_in_lds(ra);
-            const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
-            const bool io = !is_ram && ea < 0x6000;
-            const std::uint32_t rom_off = ea & 0x7FFF;
-            const std::uint32_t ram_off = base + C::ram_lds_off(ra);
-            const std::uint32_t spare = base + C::kSpare;
-            const std::uint32_t laddr0 = ram_lds ? ram_off : spare;
-            const std::uint32_t laddr = rom ? rom_off : laddr0;
-            const std::uint32_t prgram_row = ea - 0x5800;
-            const std::uint32_t row = is_ram ? ra : prgram_row;
-            const bool rd = d0 & 0x100;
-            const bool wr = (d0 & 0x200) && kind != mc::KILLEGAL;
-            const std::uint32_t ml = lds[laddr];
-            std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
-            if (rd && glob) M = s.ram[c.goff(row)];
-            if (rd && io) M = c.io_rd(ea);
-            // Adder, logic unit and right shifter.
-            const std::uint32_t R = ubfe(c.regs, d2, 8);
-            const std::uint32_t xa = (d1 & 0x20) ? M : R;
-            const std::uint32_t bsrc = (d1 & 0x40) ? xa : M;
-            const std::uint32_t xb = (bsrc & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
-            const std::uint32_t cf = c.p & 1;
-            const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
-            const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
-            const bool right = d1 & 0x200;
-            const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
-            const std::uint32_t ar = (sum & (d2 >> 24)) | lres;
-            const std::uint32_t r = right ? sr : ar;
-            const std::uint32_t c_right = xa & 1, c_add = (sum >> 8) & 1;
-            const std::uint32_t carry = right ? c_right : c_add;
-            const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
-            const std::uint32_t nv_bit = M & 0xC0, nv_alu = (r & 0x80) | ovf;
-            const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
-            const std::uint32_t f = nv | (r == 0 ? 2u : 0u) | carry;
-            const std::uint32_t fm = d0 >> 24;
-            const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
-            c.p = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
-            // Register write-back.
-            const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
-            c.regs = (c.regs & ~dmask) | ((r << doff) & dmask);
-            // Memory write: LDS RAM (non-writers store to their spare byte),
-            // HBM, or an I/O register.
-            const std::uint32_t waddr = (wr && ram_lds) ? laddr : spare;
-            lds[waddr] = static_cast<std::uint8_t>(r);
-            if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
-            if (wr && io) dots += c.io_wr(ea, r);
-            // Next PC: fall through or branch.
-            const std::uint32_t fall = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
-            const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
-            const std::uint32_t target = (fall + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
-            const std::uint32_t bdots = ((fall ^ target) & 0xFF00) ? 6u : 3u;
-            const std::uint32_t tdots = taken ? bdots : 0u;
-            dots += tdots;
-            std::uint32_t next = taken ? target : fall;
-            if (kind == mc::KCTRL) {
-                // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
-                // JSR/BRK/PHA/PHP push, RTS/RTI/PLA/PLP pull.
-                const std::uint32_t op_c = (d0 >> 19) & 15;
-                constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
-                                                  (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
-                constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
-                                                 (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
-                const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
-                const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
-                const std::uint32_t sp = c.regs >> 24;
-                const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
-                const std::uint32_t pb = c.p | 0x30;
-                const std::uint32_t areg = c.regs & 0xFF, rethi = ret >> 8, retlo = ret & 0xFF;
-                const std::uint32_t v0a = op_c == mc::PHP ? pb : rethi;
-                const std::uint32_t v0 = op_c == mc::PHA ? areg : v0a;
+        }
+        const uint4 m = reinterpret_cast<const uint4*>(lds + kLdsMicro)[op];
+        const std::uint32_t d0 = m.x, d1 = m.y, d2 = m.z, d3 = m.w;
+        const std::uint32_t kind = (d0 >> 10) & 3;
+        // Every conditional below selects between values that are already
+        // computed, so the compiler emits v_cndmask instead of divergent
+        // branches; only memory and I/O side paths branch.
+        // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
+        const std::uint32_t xreg = ubfe(c.regs, 8, 8);
+        const std::uint32_t pidx = ((op & 0x1F) == 0x01) ? xreg : 0u;
+        const std::uint32_t pz = (b1 + pidx) & 0xFF;
+        const std::uint32_t pz1 = (pz + 1) & 0xFF;
+        const std::uint32_t ptr = lds[base + pz] | (lds[base + pz1] << 8);
+        // Effective address.
+        const std::uint32_t abs = b1 | (b2 << 8);
+        const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
+        const std::uint32_t idx = ubfe(c.regs, d0, d1);
+        const std::uint32_t ea_full = ebase + idx;
+        const std::uint32_t ea_mask = (d0 & 0x40) ? 0xFFu : 0xFFFFu;
+        const std::uint32_t ea = ea_full & ea_mask;
+        const std::uint32_t cross = (((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1;
+        dots += ((d0 >> 14) & 31) + 3 * cross;
+        // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
+        // rows, PRG RAM) or the I/O registers.
+        const std::uint32_t ra = ea & 0x7FF;
+        const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
+        const bool ram_lds = is_ram && C::ram_in_lds(ra);
+        const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
+        const bool io = !is_ram && ea < 0x6000;
+        const std::uint32_t rom_off = ea & 0x7FFF;
+        const std::uint32_t ram_off = base + C::ram_lds_off(ra);
+        const std::uint32_t laddr0 = ram_lds ? ram_off : spare;
+        const std::uint32_t laddr = rom ? rom_off : laddr0;
+        const std::uint32_t prgram_row = ea - 0x5800;
+        const std::uint32_t row = is_ram ? ra : prgram_row;
+        const bool rd = d0 & 0x100;
+        const bool wr = (d0 & 0x200) && active;
+        const std::uint32_t ml = lds[laddr];
+        std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
+        if (rd && glob) M = s.ram[c.goff(row)];
+        // Work that does not depend on the operand comes first, so the
+        // operand load above is in flight meanwhile.
+        // Next PC: fall through or branch.
+        const std::uint32_t fall = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
+        const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
+        const std::uint32_t target = (fall + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
+        const std::uint32_t bdots = ((fall ^ target) & 0xFF00) ? 6u : 3u;
+        const std::uint32_t tdots = taken ? bdots : 0u;
+        dots += tdots;
+        std::uint32_t next = taken ? target : fall;
+        std::uint32_t p_c = c.p, regs_c = c.regs;
+        const bool is_ctrl = kind == mc::KCTRL;
+        if (active && kind == mc::KCTRL) {
+            // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
+            // JSR/BRK/PHA/PHP push up to 3 bytes at SP, SP-1, SP-2;
+            // RTS/RTI/PLA/PLP pull up to 3 from SP+1..SP+3.
+            const std::uint32_t op_c = (d0 >> 19) & 15;
+            constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
+                                              (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
+            constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
+                                             (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
+            const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
+            const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
+            const std::uint32_t sp = c.regs >> 24;
+            const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
+            const std::uint32_t pb = c.p | 0x30;
+            const std::uint32_t areg = c.regs & 0xFF, rethi = ret >> 8, retlo = ret & 0xFF;
+            const std::uint32_t v0a = op_c == mc::PHP ? pb : rethi;
+            const std::uint32_t v0 = op_c == mc::PHA ? areg : v0a;
+            std::uint32_t w0, w1, w2;
+            constexpr std::uint32_t kLo = kFull ? 2u : 0x82u;
+            if (sp - kLo <= 0xFCu - kLo) {
+                // The window $01(SP-2)-$01(SP+3) is in LDS without page wrap:
+                // read all six bytes, write back new or old values.
+                const std::uint32_t wb = stk + sp - 2;
+                const std::uint32_t o2 = lds[wb], o1 = lds[wb + 1], o0 = lds[wb + 2];
+                w0 = lds[wb + 3]; w1 = lds[wb + 4]; w2 = lds[wb + 5];
+                const std::uint32_t n0 = npush >= 1 ? v0 : o0;
+                const std::uint32_t n1 = npush >= 2 ? retlo : o1;
+                const std::uint32_t n2 = npush >= 3 ? pb : o2;
+                lds[wb + 2] = static_cast<std::uint8_t>(n0);
+                lds[wb + 1] = static_cast<std::uint8_t>(n1);
+                lds[wb] = static_cast<std::uint8_t>(n2);
+            } else {
                 if (npush >= 1) c.ram_wr(0x100 | sp, v0);
                 if (npush >= 2) c.ram_wr(0x100 | ((sp - 1) & 0xFF), retlo);
                 if (npush >= 3) c.ram_wr(0x100 | ((sp - 2) & 0xFF), pb);
-                std::uint32_t w0 = 0, w1 = 0, w2 = 0;
-                if (npull >= 1) w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
-                if (npull >= 2) w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
-                if (npull >= 3) w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
-                const std::uint32_t nsp = (sp - npush + npull) & 0xFF;
-                c.regs = (c.regs & 0x00FFFFFFu) | (nsp << 24);
-                const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
-                const std::uint32_t brk_p = c.p | 0x24;
-                const std::uint32_t p_b = op_c == mc::BRK ? brk_p : c.p;
-                c.p = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : p_b;
-                if (op_c == mc::PLA) {
-                    c.regs = (c.regs & ~0xFFu) | w0;
-                    c.p = (c.p & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
+                w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
+                w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
+                w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
+            }
+            const std::uint32_t nsp = (sp - npush + npull) & 0xFF;
+            regs_c = (c.regs & 0x00FFFFFFu) | (nsp << 24);
+            const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
+            const std::uint32_t brk_p = c.p | 0x24;
+            const std::uint32_t p_b = op_c == mc::BRK ? brk_p : c.p;
+            p_c = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : p_b;
+            if (op_c == mc::PLA) {
+                regs_c = (regs_c & ~0xFFu) | w0;
+                p_c = (p_c & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
+            }
+            const std::uint32_t rts_pc = ((w0 | (w1 << 8)) + 1) & 0xFFFF, rti_pc = w1 | (w2 << 8);
+            const std::uint32_t n3 = op_c == mc::BRK ? c.brk_vec : next;
+            const std::uint32_t n2 = op_c == mc::RTI ? rti_pc : n3;
+            const std::uint32_t n1 = op_c == mc::RTS ? rts_pc : n2;
+            next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs : n1;
+            if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
+                const std::uint32_t l = c.bus_rd(abs);
+                next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
+            }
+            // Idle loop (JMP to itself): the console repeats 3-cycle jumps
+            // until the next timing event; account for them in one go.
+            const std::int32_t gap = left - static_cast<std::int32_t>(dots);
+            if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
+                std::int32_t k = (gap + 8) / 9;
+                if (kBudget) {
+                    const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
+                    k = k < room ? k : room;
                 }
-                const std::uint32_t rts_pc = ((w0 | (w1 << 8)) + 1) & 0xFFFF, rti_pc = w1 | (w2 << 8);
-                const std::uint32_t n3 = op_c == mc::BRK ? c.brk_vec : next;
-                const std::uint32_t n2 = op_c == mc::RTI ? rti_pc : n3;
-                const std::uint32_t n1 = op_c == mc::RTS ? rts_pc : n2;
-                next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs : n1;
-                if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
-                    const std::uint32_t l = c.bus_rd(abs);
-                    next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
-                }
-                // Idle loop (JMP to itself): the console repeats 3-cycle jumps
-                // until the next timing event; account for them in one go.
-                const std::int32_t gap = left - static_cast<std::int32_t>(dots);
-                if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
-                    std::int32_t k = (gap + 8) / 9;
-                    if (kBudget) {
-                        const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
-                        k = k < room ? k : room;
-                    }
-                    dots += 9u * static_cast<std::uint32_t>(k);
-                    in_frame += static_cast<std::uint32_t>(k);
-                    instructions += static_cast<std::uint64_t>(k);
-                    if constexpr (kStats == 2) {
-                        atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
-                        atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
-                    }
+                dots += 9u * static_cast<std::uint32_t>(k);
+                in_frame += static_cast<std::uint32_t>(k);
+                instructions += static_cast<std::uint64_t>(k);
+                if constexpr (kStats == 2) {
+                    atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
+                    atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
                 }
             }
-            if (kind == mc::KILLEGAL) {  // the console freezes before executing it
-                c.fault |= 1;
-                active = false;
-                next = pc0;
-                dots = 0;
-            }
-            c.pc = next;
-            if constexpr (kStats == 2) {
+        }
+        if (rd && io && active) M = c.io_rd(ea);
+        // Adder, logic unit and right shifter.
+        const std::uint32_t R = ubfe(c.regs, d2, 8);
+        const std::uint32_t xa = (d1 & 0x20) ? M : R;
+        const std::uint32_t bsrc = (d1 & 0x40) ? xa : M;
+        const std::uint32_t xb = (bsrc & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
+        const std::uint32_t cf = c.p & 1;
+        const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
+        const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
+        const bool right = d1 & 0x200;
+        const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
+        const std::uint32_t ar = (sum & (d2 >> 24)) | lres;
+        const std::uint32_t r = right ? sr : ar;
+        const std::uint32_t c_right = xa & 1, c_add = (sum >> 8) & 1;
+        const std::uint32_t carry = right ? c_right : c_add;
+        const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
+        const std::uint32_t nv_bit = M & 0xC0, nv_alu = (r & 0x80) | ovf;
+        const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
+        const std::uint32_t f = nv | (r == 0 ? 2u : 0u) | carry;
+        const std::uint32_t fm = d0 >> 24;
+        const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
+        const std::uint32_t pn = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
+        // Register write-back (a control opcode's own results win).
+        const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
+        const std::uint32_t regs_n = (c.regs & ~dmask) | ((r << doff) & dmask);
+        // Memory write: LDS RAM (non-writers store to their spare byte), HBM
+        // (non-writers store to their trash byte), or an I/O register.
+        const std::uint32_t waddr = (wr && ram_lds) ? laddr : spare;
+        lds[waddr] = static_cast<std::uint8_t>(r);
+        if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
+        if (wr && io) dots += c.io_wr(ea, r);
+        p_c = is_ctrl ? p_c : pn;
+        regs_c = is_ctrl ? regs_c : regs_n;
+        // Commit (an illegal opcode freezes the console before it executes).
+        const bool legal = kind != mc::KILLEGAL;
+        const bool commit = active && legal;
+        c.pc = commit ? next : c.pc;
+        c.regs = commit ? regs_c : c.regs;
+        c.p = commit ? p_c : c.p;
+        c.flags |= (active && !legal) ? kFault : 0u;
+        const std::uint32_t counted = commit ? 1u : 0u;
+        in_frame += counted;
+        instructions += counted;
+        if constexpr (kStats == 2) {
+            if (commit) {
                 atomicAdd(&s.prof_opcodes[op], 1ull);
                 atomicAdd(&s.prof_pcs[pc0], 1ull);
             }
-            const std::uint32_t counted = kind != mc::KILLEGAL ? 1u : 0u;  // a fault is not an instruction
-            in_frame += counted;
-            instructions += counted;
-            left -= static_cast<std::int32_t>(dots);
-            if (left <= 0) {  // a timing event was crossed: settle the PPU
-                const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
-                horizon = to_event(c.r32(reg::kFrameDot));
-                left = static_cast<std::int32_t>(horizon);
-                if (fc) {
-                    ++frames;
-                    in_frame = 0;
-                    if (--frames_left == 0) active = false;
-                }
-            }
-            if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
-                const std::uint32_t fc = c.settle(horizon - static_cast<std::uint32_t>(left));
-                horizon = to_event(c.r32(reg::kFrameDot));
-                left = static_cast<std::int32_t>(horizon);
-                frames += fc;
-                budget_hits += fc ? 0u : 1u;
+        }
+        active = commit;
+        left -= commit ? static_cast<std::int32_t>(dots) : 0;
+        if (active && left <= 0) {  // a timing event was crossed: settle the PPU
+            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
+            const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
+            c.w32(reg::kHorizon, h);
+            left = static_cast<std::int32_t>(h);
+            if (fc) {
+                c.w32(reg::kFrames, c.r32(reg::kFrames) + 1);
                 in_frame = 0;
-                if (--frames_left == 0) active = false;
+                const std::uint32_t fl = c.r32(reg::kFramesLeft) - 1;
+                c.w32(reg::kFramesLeft, fl);
+                if (fl == 0) active = false;
             }
+        }
+        if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
+            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
+            const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
+            c.w32(reg::kHorizon, h);
+            left = static_cast<std::int32_t>(h);
+            c.w32(reg::kFrames, c.r32(reg::kFrames) + fc);
+            c.w32(reg::kBudgetHits, c.r32(reg::kBudgetHits) + (fc ? 0u : 1u));
+            in_frame = 0;
+            const std::uint32_t fl = c.r32(reg::kFramesLeft) - 1;
+            c.w32(reg::kFramesLeft, fl);
+            if (fl == 0) active = false;
         }
         // OAM DMA ($4014, console.hpp:191-197): the whole wave copies one
         // console's 256 bytes at a time, 4 per lane.  RAM, PRG RAM and PRG ROM
         // pages have no read side effects; I/O pages are read by the console's
         // own lane through the bus, in order.
-        std::uint64_t req = __ballot(c.dma != 0);
+        std::uint64_t req = __ballot((c.flags & kDmaPending) != 0);
         while (req != 0) {
             const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(req)) - 1);
             req &= req - 1;
-            const std::uint32_t page = __builtin_amdgcn_readlane(c.dma, src) & 0xFF;
             const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
-            const std::uint32_t e_base = __builtin_amdgcn_readlane(c.base, src);
-            const std::uint32_t oa = lds[e_base + C::kRegs + reg::kOamAddr];
+            const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
+            const std::uint32_t page = lds[e_regs + reg::kDmaPage];
+            const std::uint32_t oa = lds[e_regs + reg::kOamAddr];
+            const std::uint32_t e_base = e_regs - C::kRegs;
             if (page < 0x20 || page >= 0x60) {
                 for (std::uint32_t k = 0; k < 4; ++k) {
                     const std::uint32_t i = 4 * lane + k;
                     const std::uint32_t addr = (page << 8) | i;
                     std::uint32_t val;
                     if (page < 0x20) {
-                        const std::uint32_t ra = addr & 0x7FF;
-                        val = C::ram_in_lds(ra) ? lds[e_base + C::ram_lds_off(ra)] : s.ram[__umul24(ra, P) + e_env];
+                        const std::uint32_t ra2 = addr & 0x7FF;
+                        val = C::ram_in_lds(ra2) ? lds[e_base + C::ram_lds_off(ra2)] : s.ram[__umul24(ra2, P) + e_env];
                     } else if (page < 0x80) {
                         val = s.ram[__umul24(addr - 0x5800, P) + e_env];
                     } else {
@@ -665,11 +721,14 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
                 c.w8(reg::kOamAddr, oa);
             }
         }
-        c.dma = 0;
+        c.flags &= ~kDmaPending;
     }
 
     if (!mine) return;
-    if (left != static_cast<std::int32_t>(horizon)) frames += c.settle(horizon - static_cast<std::uint32_t>(left));
+    // Settle the dots of instructions executed since the last event (only a
+    // console that faulted stops between events).
+    if (left != static_cast<std::int32_t>(c.r32(reg::kHorizon)))
+        c.w32(reg::kFrames, c.r32(reg::kFrames) + c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left)));
 
     // Write the LDS-resident RAM rows and registers back to HBM.
     {
@@ -690,6 +749,7 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
         }
     }
     const std::uint32_t fd = c.r32(reg::kFrameDot);
+    const std::uint32_t frames = c.r32(reg::kFrames);
     s.pc[env] = static_cast<std::uint16_t>(c.pc);
     s.a[env] = static_cast<std::uint8_t>(c.regs);
     s.x[env] = static_cast<std::uint8_t>(c.regs >> 8);
@@ -701,7 +761,7 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
     s.cycles[env] += advanced / 3;
     s.frame[env] += frames;
     s.frame_dot[env] = fd;
-    s.nmi_pending[env] = static_cast<std::uint8_t>(c.nmi);
+    s.nmi_pending[env] = static_cast<std::uint8_t>((c.flags & kNmiPending) ? 1 : 0);
     s.status[env] = static_cast<std::uint8_t>(c.r8(reg::kStatus));
     s.ctrl[env] = static_cast<std::uint8_t>(c.r8(reg::kCtrl));
     s.mask[env] = static_cast<std::uint8_t>(c.r8(reg::kMask));
@@ -719,17 +779,18 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
     s.c1_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Count));
     s.strobe[env] = static_cast<std::uint8_t>(c.r8(reg::kStrobe));
     s.c2_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC2Count));
-    s.fault[env] = static_cast<std::uint8_t>(c.fault);
+    const bool fault = (c.flags & kFault) != 0;
+    s.fault[env] = static_cast<std::uint8_t>(fault ? 1 : 0);
 
     float reward = 0.0f;
     std::uint32_t done = 1;
-    if (!c.fault) reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
+    if (!fault) reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
     s.rewards[env] = reward;
     s.done[env] = static_cast<std::uint8_t>(done);
     if constexpr (kStats != 0) {
         s.stat_instructions[env] = instructions;
         s.stat_frames[env] = frames;
-        s.stat_budget_hits[env] = budget_hits;
+        s.stat_budget_hits[env] = c.r32(reg::kBudgetHits);
     }
     if (auto_reset && done) {
         reset_env(s, env, lds);
@@ -738,17 +799,20 @@ __global__ void __launch_bounds__(kBlock) step_kernel(DeviceState s, std::uint32
 }
 
 struct Geometry {
-    std::uint32_t lane_bits, consoles, blocks, lds;
+    std::uint32_t waves, lane_bits, consoles, blocks, lds;
     bool full;
 };
 
-Geometry geometry(std::uint32_t n) {
-    // One wave per SIMD: 1,024 waves on MI355X's 256 CUs.
+// W waves per workgroup (one workgroup per CU), L consoles per wave: the
+// smallest power-of-two L with 256 CUs x W x L >= n.  W trades issue slots for
+// latency hiding: W/4 waves share each SIMD.
+Geometry geometry(std::uint32_t n, std::uint32_t waves) {
     std::uint32_t lane_bits = 0;
-    while (lane_bits < 6 && (1024u << lane_bits) < n) ++lane_bits;
+    while (lane_bits < 6 && ((256u * waves) << lane_bits) < n) ++lane_bits;
     Geometry g{};
+    g.waves = waves;
     g.lane_bits = lane_bits;
-    g.consoles = 4u << lane_bits;
+    g.consoles = waves << lane_bits;
     g.blocks = (n + g.consoles - 1) / g.consoles;
     g.full = lds_bytes(g.consoles, true) <= kLdsLimit;
     g.lds = lds_bytes(g.consoles, g.full);
@@ -761,8 +825,8 @@ hipError_t launch_variant(const DeviceState& s, const Geometry& g, std::uint32_t
     const void* fn = reinterpret_cast<const void*>(&step_kernel<kStats, kFull, kBudget>);
     const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(g.lds));
     if (e != hipSuccess) return e;
-    step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(kBlock), g.lds, stream>>>(s, frameskip, max_instr,
-                                                                                         auto_reset, g.lane_bits);
+    step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(64 * g.waves), g.lds, stream>>>(
+        s, frameskip, max_instr, auto_reset, g.lane_bits);
     return hipGetLastError();
 }
 
@@ -773,11 +837,21 @@ hipError_t launch_mode(const DeviceState& s, const Geometry& g, std::uint32_t fr
                   : launch_variant<kStats, false, kBudget>(s, g, frameskip, max_instr, auto_reset, stream);
 }
 
+// Waves per workgroup: NESLE_WAVES_PER_GROUP (4, 8 or 16) overrides the default.
+std::uint32_t waves_per_group() {
+    static const std::uint32_t w = [] {
+        const char* e = std::getenv("NESLE_WAVES_PER_GROUP");
+        const long v = e != nullptr ? std::strtol(e, nullptr, 10) : 0;
+        return (v == 4 || v == 8 || v == 16) ? static_cast<std::uint32_t>(v) : 4u;
+    }();
+    return w;
+}
+
 }  // namespace
 
 hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, bool auto_reset,
                        int stats_mode, hipStream_t stream) {
-    const Geometry g = geometry(s.n);
+    const Geometry g = geometry(s.n, waves_per_group());
     const std::uint32_t ar = auto_reset ? 1u : 0u;
     // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
     const bool budget = max_instr < 15000;
