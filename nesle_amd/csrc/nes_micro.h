@@ -1,15 +1,20 @@
 // nes_micro.h -- the 6502 microcode of the step kernel (nes_step.hip).
 //
-// One 128-bit word per opcode (four dwords d[0..3]) drives a single
+// One 64-byte word (sixteen dwords d[0..15]) per opcode drives a single
 // branch-free datapath: effective address, operand, an adder / logic unit /
-// right shifter, flag merge, register write-back and next PC.  Stack and
-// control-transfer opcodes set kind = CTRL and take the kernel's stack path.
+// right shifter, flag merge, register write-back, a three-byte stack window
+// (pushes, pulls, stack-pointer change) and the next-PC selection.  Besides
+// the 256 opcodes there are two virtual entries: kNopEntry (a lane that has
+// finished its frames: changes nothing) and kNmiEntry (NMI entry: pushes PC
+// and P like BRK and is counted as no instruction).
 //
 // CPU registers live packed in one VGPR: A bits 0-7, X 8-15, Y 16-23, SP
 // 24-31.  Register operands are read with a bitfield extract whose offset and
 // width come straight from a microcode dword: the hardware uses only the low
 // five bits of those operands, so fields placed at bit 0 of a dword cost no
-// extraction.
+// extraction.  Masks that select between 8- or 16-bit values only need their
+// low bits; whole-dword fields (push mask, perm selector, SP delta, register
+// mask) are used as they are.
 //
 // Field map:
 //   d0  0-4  index-register offset in the packed registers (X 8, Y 16)
@@ -17,10 +22,8 @@
 //       6    wrap the effective address to the zero page
 //       7    +1 cycle when indexing crosses a page
 //       8    reads the memory operand         9  writes the memory operand
-//       10-11 kind (ALU, BRANCH, CTRL, ILLEGAL)
-//       12-13 length in bytes               14-18 base cycles x 3 (PPU dots)
-//       19-22 control op                    23   BIT flag rule
-//       24-31 flags taken from the datapath (N V . . . . Z C)
+//       12-13 length in bytes               14-18 base CPU cycles
+//       23   BIT flag rule                  24-31 flags taken from the datapath
 //   d1  0-4  index width (8 when indexed, else 0)
 //       5    adder input A is the operand M (else register R)
 //       6    adder input B is taken from A (left shifts: A + A + c)
@@ -35,8 +38,27 @@
 //       16-23 mask of R ^ M (XOR term)       24-31 result mask of the adder
 //   d3  0-4  branch test width (1 for branches, 0 otherwise)
 //       5-9  destination offset in the packed registers
-//       10-14 destination width (8, or 0 for none)
 //       16-23 flags AND mask                 24-31 flags OR mask (| 0x20)
+//   d4  push mask over the window bytes in memory order (byte 0 = $0100+SP-2,
+//       byte 1 = SP-1, byte 2 = SP)
+//   d5  v_perm selector building the pushed bytes from
+//       {src0 = (registers << 8) | pushed P, src1 = return address}
+//   d6  stack-pointer change << 24
+//   d7  interrupt vector (BRK, NMI; filled in from the PRG image at launch)
+//   d8  destination register mask in the packed registers
+//   d9  next PC := absolute operand (JMP, JSR)            0xFFFF or 0
+//   d10 next PC := pulled return address (RTS, RTI)       0xFFFF or 0
+//   d11 next PC := vector (BRK, NMI)                      0xFFFF or 0
+//   d12 0-4 shift of the pulled bytes (RTI 8), 16 +1 (RTS), 24-25 return
+//       address offset from the opcode (JSR, BRK 2)
+//   d13 0-7 operand := first pulled byte (PLA, PLP, RTI)
+//       8-15 lowest SP the window serves, 16-23 SP range above it: outside
+//       it the stack bytes leave the LDS window and the opcode takes the
+//       kernel's stack side path
+//   d14 0 counts as an instruction, 1 clears the pending NMI,
+//       2 JMP absolute (idle-loop check), 3 JMP indirect (side path),
+//       4 illegal opcode
+//   d15 0-7 P := pulled byte (PLP, RTI), 8-15 B/U bits of a pushed P
 #pragma once
 
 #include <cstdint>
@@ -44,15 +66,18 @@
 namespace nesle {
 namespace mc {
 
-enum Kind : std::uint32_t { KALU = 0, KBRANCH = 1, KCTRL = 2, KILLEGAL = 3 };
-enum Ctrl : std::uint32_t { JMPA = 0, JMPI, JSR, RTS, RTI, BRK, PHA, PHP, PLA, PLP };
+constexpr std::uint32_t kDwords = 16;
+constexpr std::uint32_t kNopEntry = 256, kNmiEntry = 257, kEntries = 258;
+// d14 bits.
+constexpr std::uint32_t kCount = 1, kClearNmi = 2, kJmpAbs = 4, kJmpInd = 8, kIllegal = 16;
+
 enum Mode : std::uint32_t { IMP = 0, ACC, IMM, ZP, ZPX, ZPY, ABS, ABSX, ABSY, INDX, INDY, IND, REL };
 enum Reg : std::uint32_t { RA = 0, RX = 1, RY = 2, RSP = 3, RNONE = 4 };
 
 constexpr std::uint32_t kN = 0x80, kV = 0x40, kZ = 0x02, kC = 0x01;
 
 struct Word {
-    std::uint32_t d[4] = {0, 0, 0, 0};
+    std::uint32_t d[kDwords] = {};
     constexpr Word& set(int dw, int lo, int bits, std::uint32_t v) {
         const std::uint32_t m = (bits == 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u)) << lo;
         d[dw] = (d[dw] & ~m) | ((v << lo) & m);
@@ -66,9 +91,28 @@ constexpr std::uint32_t mode_len(std::uint32_t m) {
 
 constexpr std::uint32_t reg_off(std::uint32_t r) { return r == RNONE ? 0u : 8u * r; }
 
-// Common part: addressing mode, kind, length, cycles.
-constexpr Word base(std::uint32_t mode, std::uint32_t cycles, bool penalty, std::uint32_t kind) {
+// Stack window range: the opcode's pushed and pulled bytes stay inside the
+// console's LDS copy of the stack page ($0100-$01FF when all RAM is in LDS,
+// $0180-$01FF otherwise) without wrapping.
+constexpr Word window(Word w, std::uint32_t npush, std::uint32_t npull, bool full) {
+    const std::uint32_t lo = full ? (npush ? npush - 1u : 0u) : 0x82u;
+    const std::uint32_t hi = 0xFFu - npull;
+    w.set(13, 8, 8, lo);
+    w.set(13, 16, 8, hi - lo);
+    return w;
+}
+
+constexpr Word make_nop() {
     Word w;
+    w.set(3, 16, 8, 0xFF);   // flags AND mask: keep
+    w.set(3, 24, 8, 0x20);   // flags OR mask: the unused bit reads as 1
+    w.set(13, 16, 8, 0xFF);  // any SP is served
+    return w;
+}
+
+// Common part: addressing mode, length, cycles; no stack use.
+constexpr Word base(std::uint32_t mode, std::uint32_t cycles, bool penalty) {
+    Word w = make_nop();
     const bool idx_x = mode == ZPX || mode == ABSX;
     const bool idx_y = mode == ZPY || mode == ABSY || mode == INDY;
     w.set(0, 0, 5, idx_x ? 8u : (idx_y ? 16u : 0u));
@@ -76,11 +120,9 @@ constexpr Word base(std::uint32_t mode, std::uint32_t cycles, bool penalty, std:
     w.set(0, 5, 1, (mode == INDX || mode == INDY) ? 1u : 0u);
     w.set(0, 6, 1, (mode == ZP || mode == ZPX || mode == ZPY) ? 1u : 0u);
     w.set(0, 7, 1, penalty ? 1u : 0u);
-    w.set(0, 10, 2, kind);
     w.set(0, 12, 2, mode_len(mode));
-    w.set(0, 14, 5, 3u * cycles);
-    w.set(3, 16, 8, 0xFF);   // flags AND mask: keep
-    w.set(3, 24, 8, 0x20);   // flags OR mask: the unused bit reads as 1
+    w.set(0, 14, 5, cycles);
+    w.set(14, 0, 5, kCount);
     return w;
 }
 
@@ -101,7 +143,7 @@ constexpr Word adder(Word w, bool a_is_m, std::uint32_t reg, bool b_from_a, std:
 constexpr Word dest(Word w, std::uint32_t reg, std::uint32_t flags) {
     if (reg != RNONE) {
         w.set(3, 5, 5, reg_off(reg));
-        w.set(3, 10, 5, 8);
+        w.set(8, 0, 32, 0xFFu << reg_off(reg));
     }
     w.set(0, 24, 8, flags);
     return w;
@@ -115,7 +157,7 @@ constexpr Word memops(Word w, bool rd, bool wr) {
 
 // R <- M (LDA/LDX/LDY).
 constexpr Word load(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint32_t dst) {
-    Word w = base(mode, cyc, pen, KALU);
+    Word w = base(mode, cyc, pen);
     w = memops(w, mode != IMM, false);
     w = adder(w, true, RNONE, false, 0, 0, false, false);
     return dest(w, dst, kN | kZ);
@@ -123,21 +165,21 @@ constexpr Word load(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint32
 
 // M <- R (STA/STX/STY).
 constexpr Word store(std::uint32_t mode, std::uint32_t cyc, std::uint32_t reg) {
-    Word w = base(mode, cyc, false, KALU);
+    Word w = base(mode, cyc, false);
     w = memops(w, false, true);
     return adder(w, false, reg, false, 0, 0, false, false);
 }
 
 // Register transfers, increments and decrements: dst <- R + B + cin.
 constexpr Word regop(std::uint32_t reg, std::uint32_t dst, std::uint32_t b_xor, bool cin_1, bool flags) {
-    Word w = base(IMP, 2, false, KALU);
+    Word w = base(IMP, 2, false);
     w = adder(w, false, reg, false, 0, b_xor, cin_1, false);
     return dest(w, dst, flags ? (kN | kZ) : 0u);
 }
 
 // ADC / SBC / CMP / CPX / CPY.
 constexpr Word arith(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint32_t reg, bool subtract, bool compare) {
-    Word w = base(mode, cyc, pen, KALU);
+    Word w = base(mode, cyc, pen);
     w = memops(w, mode != IMM, false);
     w = adder(w, false, reg, false, 0xFF, subtract ? 0xFFu : 0u, compare, !compare);
     return dest(w, compare ? RNONE : RA, compare ? (kN | kZ | kC) : (kN | kZ | kC | kV));
@@ -146,7 +188,7 @@ constexpr Word arith(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint3
 // ORA / AND / EOR / BIT: r = (R & M & and_mask) | ((R ^ M) & xor_mask).
 constexpr Word logic(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint32_t and_mask, std::uint32_t xor_mask,
                      bool bit_rule) {
-    Word w = base(mode, cyc, pen, KALU);
+    Word w = base(mode, cyc, pen);
     w = memops(w, mode != IMM, false);
     w.set(2, 0, 5, 0);        // R = A
     w.set(2, 8, 8, and_mask);
@@ -157,7 +199,7 @@ constexpr Word logic(std::uint32_t mode, std::uint32_t cyc, bool pen, std::uint3
 
 // ASL / ROL (adder: A + A + c), LSR / ROR (right shifter), on A or memory.
 constexpr Word shift(std::uint32_t mode, std::uint32_t cyc, bool right, bool rot) {
-    Word w = base(mode, cyc, false, KALU);
+    Word w = base(mode, cyc, false);
     const bool mem = mode != ACC;
     w = memops(w, mem, mem);
     if (right) {
@@ -173,21 +215,21 @@ constexpr Word shift(std::uint32_t mode, std::uint32_t cyc, bool right, bool rot
 
 // INC / DEC memory: M + 0 + 1 or M + 0xFF + 0.
 constexpr Word incdec(std::uint32_t mode, std::uint32_t cyc, bool dec) {
-    Word w = base(mode, cyc, false, KALU);
+    Word w = base(mode, cyc, false);
     w = memops(w, true, true);
     w = adder(w, true, RNONE, false, 0, dec ? 0xFFu : 0u, !dec, false);
     return dest(w, RNONE, kN | kZ);
 }
 
 constexpr Word flagop(std::uint32_t and_mask, std::uint32_t or_mask) {
-    Word w = base(IMP, 2, false, KALU);
+    Word w = base(IMP, 2, false);
     w.set(3, 16, 8, and_mask);
     w.set(3, 24, 8, or_mask | 0x20u);
     return w;
 }
 
 constexpr Word branch(std::uint32_t op) {
-    Word w = base(REL, 2, false, KBRANCH);
+    Word w = base(REL, 2, false);
     // Opcode xxy10000 tests N, V, C, Z (bits 7-6) and is taken when the flag
     // equals y: XOR the flag with !y, then the tested bit is 1 when taken.
     constexpr std::uint32_t pos[4] = {7, 6, 0, 1};
@@ -199,21 +241,40 @@ constexpr Word branch(std::uint32_t op) {
     return w;
 }
 
-constexpr Word ctrl(std::uint32_t op, std::uint32_t mode, std::uint32_t cyc) {
-    Word w = base(mode, cyc, false, KCTRL);
-    w.set(0, 19, 4, op);
-    return w;
+// Stack and control transfer (cpu.hpp:394-402,603-606,666-694 and the NMI
+// entry cpu.hpp:112-123).  Pushes go to SP, SP-1, SP-2; pulls come from
+// SP+1, SP+2, SP+3.
+constexpr std::uint32_t kPermZero = 0x0C;  // v_perm selector byte for 0x00
+constexpr std::uint32_t perm_sel(std::uint32_t b0, std::uint32_t b1, std::uint32_t b2) {
+    return b0 | (b1 << 8) | (b2 << 16) | (kPermZero << 24);
+}
+// Selector bytes: 0 return address low, 1 return address high, 4 pushed P, 5 A.
+constexpr Word pushes(Word w, std::uint32_t n, std::uint32_t sel, std::uint32_t ret_off, std::uint32_t bflags,
+                      bool full) {
+    w.set(4, 0, 32, n == 1 ? 0x00FF0000u : (n == 2 ? 0x00FFFF00u : 0x00FFFFFFu));
+    w.set(5, 0, 32, sel);
+    w.set(6, 0, 32, static_cast<std::uint32_t>(-static_cast<std::int32_t>(n)) << 24);
+    w.set(12, 24, 2, ret_off);
+    w.set(15, 8, 8, bflags);
+    return window(w, n, 0, full);
+}
+constexpr Word pulls(Word w, std::uint32_t n, bool full) {
+    w.set(6, 0, 32, n << 24);
+    w.set(13, 0, 8, 0xFF);   // operand := first pulled byte
+    return window(w, 0, n, full);
 }
 
 struct Table {
-    Word e[256];
+    Word e[kEntries];
 };
 
 // The official 151 opcodes with the reference's cycle counts
-// (cpp/include/nesle/cpu.hpp:190-353); the rest are illegal.
-constexpr Table make_table() {
+// (cpp/include/nesle/cpu.hpp:190-353); the rest are illegal.  `full`: all of
+// the console's RAM is in LDS (selects the stack window range).
+constexpr Table make_table(bool full) {
     Table t{};
-    for (auto& e : t.e) e = base(IMP, 0, false, KILLEGAL);
+    for (auto& e : t.e) e = make_nop().set(14, 0, 5, kIllegal);
+    t.e[kNopEntry] = make_nop();
     // cc=01 group over its eight addressing modes.
     const std::uint32_t modes[8] = {INDX, ZP, IMM, ABS, INDY, ZPX, ABSY, ABSX};
     const std::uint32_t cyc[8] = {6, 3, 2, 4, 5, 4, 4, 4};
@@ -267,26 +328,46 @@ constexpr Table make_table() {
     t.e[0xC8] = regop(RY, RY, 0, true, true);     // INY
     t.e[0xCA] = regop(RX, RX, 0xFF, false, true); // DEX
     t.e[0x88] = regop(RY, RY, 0xFF, false, true); // DEY
-    t.e[0xEA] = base(IMP, 2, false, KALU);        // NOP
+    t.e[0xEA] = base(IMP, 2, false);              // NOP
     t.e[0x18] = flagop(0xFE, 0x00); t.e[0x38] = flagop(0xFF, 0x01);  // CLC SEC
     t.e[0x58] = flagop(0xFB, 0x00); t.e[0x78] = flagop(0xFF, 0x04);  // CLI SEI
     t.e[0xB8] = flagop(0xBF, 0x00);                                  // CLV
     t.e[0xD8] = flagop(0xF7, 0x00); t.e[0xF8] = flagop(0xFF, 0x08);  // CLD SED
     for (std::uint32_t i = 0; i < 8; ++i) t.e[(i << 5) | 0x10u] = branch((i << 5) | 0x10u);
-    t.e[0x4C] = ctrl(JMPA, ABS, 3);
-    t.e[0x6C] = ctrl(JMPI, IND, 5);
-    t.e[0x20] = ctrl(JSR, ABS, 6);
-    t.e[0x60] = ctrl(RTS, IMP, 6);
-    t.e[0x40] = ctrl(RTI, IMP, 6);
-    t.e[0x00] = ctrl(BRK, IMP, 7);
-    t.e[0x48] = ctrl(PHA, IMP, 3);
-    t.e[0x08] = ctrl(PHP, IMP, 3);
-    t.e[0x68] = ctrl(PLA, IMP, 4);
-    t.e[0x28] = ctrl(PLP, IMP, 4);
+
+    // JMP abs: next PC = operand (and the idle-loop check).
+    t.e[0x4C] = base(ABS, 3, false).set(9, 0, 32, 0xFFFF).set(14, 0, 5, kCount | kJmpAbs);
+    // JMP (ind): the kernel's side path reads the pointer with the page-wrap bug.
+    t.e[0x6C] = base(IND, 5, false).set(14, 0, 5, kCount | kJmpInd);
+    // JSR: push PC+2 (high at SP, low at SP-1), next PC = operand.
+    t.e[0x20] = pushes(base(ABS, 6, false), 2, perm_sel(kPermZero, 0, 1), 2, 0, full).set(9, 0, 32, 0xFFFF);
+    // RTS: pull low, high; next PC = pulled + 1.
+    t.e[0x60] = pulls(base(IMP, 6, false), 2, full).set(10, 0, 32, 0xFFFF).set(12, 16, 1, 1).set(13, 0, 8, 0);
+    // RTI: pull P, low, high.
+    t.e[0x40] = pulls(base(IMP, 6, false), 3, full).set(10, 0, 32, 0xFFFF).set(12, 0, 5, 8).set(15, 0, 8, 0xFF);
+    // BRK: push PC+2 and P|B|U, set I, next PC = IRQ/BRK vector.
+    t.e[0x00] = pushes(base(IMP, 7, false), 3, perm_sel(4, 0, 1), 2, 0x30, full).set(11, 0, 32, 0xFFFF)
+                    .set(3, 24, 8, 0x24);
+    // PHA, PHP (P|B|U).
+    t.e[0x48] = pushes(base(IMP, 3, false), 1, perm_sel(kPermZero, kPermZero, 5), 0, 0, full);
+    t.e[0x08] = pushes(base(IMP, 3, false), 1, perm_sel(kPermZero, kPermZero, 4), 0, 0x30, full);
+    // PLA: A = pulled byte, N and Z.
+    {
+        Word w = pulls(base(IMP, 4, false), 1, full);
+        w = adder(w, true, RNONE, false, 0, 0, false, false);
+        t.e[0x68] = dest(w, RA, kN | kZ);
+    }
+    // PLP: P = pulled byte (B clear, U set).
+    t.e[0x28] = pulls(base(IMP, 4, false), 1, full).set(15, 0, 8, 0xFF);
+    // NMI entry: push PC and P with B clear, set I, next PC = NMI vector; not
+    // an instruction of its own (console.hpp:108-135).
+    t.e[kNmiEntry] = pushes(base(IMP, 7, false), 3, perm_sel(4, 0, 1), 0, 0x20, full).set(11, 0, 32, 0xFFFF)
+                         .set(3, 24, 8, 0x24).set(0, 12, 2, 0).set(14, 0, 5, kClearNmi);
     return t;
 }
 
-inline constexpr Table kTable = make_table();
+inline constexpr Table kTableSplit = make_table(false);
+inline constexpr Table kTableFull = make_table(true);
 
 }  // namespace mc
 }  // namespace nesle

@@ -45,27 +45,19 @@
 namespace nesle {
 namespace {
 
-__constant__ uint4 c_micro[256] = {
-#define NESLE_W(i) {mc::kTable.e[i].d[0], mc::kTable.e[i].d[1], mc::kTable.e[i].d[2], mc::kTable.e[i].d[3]}
-#define NESLE_W8(i) NESLE_W(i), NESLE_W(i + 1), NESLE_W(i + 2), NESLE_W(i + 3), NESLE_W(i + 4), NESLE_W(i + 5), \
-                    NESLE_W(i + 6), NESLE_W(i + 7)
-#define NESLE_W64(i) NESLE_W8(i), NESLE_W8(i + 8), NESLE_W8(i + 16), NESLE_W8(i + 24), NESLE_W8(i + 32), \
-                     NESLE_W8(i + 40), NESLE_W8(i + 48), NESLE_W8(i + 56)
-    NESLE_W64(0), NESLE_W64(64), NESLE_W64(128), NESLE_W64(192)
-#undef NESLE_W64
-#undef NESLE_W8
-#undef NESLE_W
-};
+__constant__ mc::Table c_micro_split = mc::kTableSplit;
+__constant__ mc::Table c_micro_full = mc::kTableFull;
 
 extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 
 constexpr std::uint32_t kMaxBlock = 1024;       // up to 16 waves per workgroup
-constexpr std::uint32_t kLdsMicro = 32768;      // 256 x 16 B
-constexpr std::uint32_t kLdsRam = 32768 + 4096; // console RAM blocks
+constexpr std::uint32_t kMicroBytes = 4 * mc::kDwords;                 // 64 B per entry
+constexpr std::uint32_t kLdsMicro = 32768;                               // after the PRG image
+constexpr std::uint32_t kLdsRam = kLdsMicro + mc::kEntries * kMicroBytes; // console RAM blocks
 // Per-console LDS block: RAM rows, 4 spare bytes, then a 40-byte register
 // area (PPU/pad registers and the rarely touched loop state).  Strides are an
 // odd number of dwords, so lanes at equal offsets hit distinct banks.
-constexpr std::uint32_t kSplitStride = 428;     // $0000-$00FF, $0180-$01FF, spare, registers
+constexpr std::uint32_t kSplitStride = 428;     // $0180-$01FF, $0000-$00FF, spare, registers
 constexpr std::uint32_t kFullStride = 2092;     // $0000-$07FF, spare, registers
 // Register area offsets (bytes from the start of the area).
 namespace reg {
@@ -84,8 +76,13 @@ constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4;
 constexpr std::uint32_t kTrashRow = kRamBytes + kPrgRamBytes;
 constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 
+// Lanes without a console run the datapath on a dummy block after the last
+// console's (they write only their own stack window and spare byte).  The
+// operand candidate read from a split block can reach 0x1FF bytes into a
+// 428-byte block; the slack keeps the dummy block's reads in bounds.
+constexpr std::uint32_t kLdsSlack = 128;
 constexpr std::uint32_t lds_bytes(std::uint32_t consoles, bool full) {
-    return kLdsRam + consoles * (full ? kFullStride : kSplitStride);
+    return kLdsRam + (consoles + 1) * (full ? kFullStride : kSplitStride) + kLdsSlack;
 }
 
 // XCD k (workgroups dispatched round-robin, b % 8 == k) owns one contiguous
@@ -93,6 +90,18 @@ constexpr std::uint32_t lds_bytes(std::uint32_t consoles, bool full) {
 __device__ __forceinline__ std::uint32_t xcd_block(std::uint32_t b, std::uint32_t nb) {
     const std::uint32_t q = nb >> 3, r = nb & 7, xcd = b & 7;
     return xcd * q + (xcd < r ? xcd : r) + (b >> 3);
+}
+
+// Wait for this wave's outstanding vector-memory operations (s_waitcnt
+// vmcnt(0), gfx9 encoding with expcnt and lgkmcnt left open).  A side path
+// that loads from HBM ends with it, so values it hands to the hot loop are
+// complete there and the loop header carries no vmcnt wait, which would
+// also wait for the store the previous iteration just issued.
+__device__ __forceinline__ void vmem_settled() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Bitwise select: bits of `a` where `m` is set, else bits of `b` (v_bfi_b32).
+__device__ __forceinline__ std::uint32_t sel(std::uint32_t m, std::uint32_t a, std::uint32_t b) {
+    return (a & m) | (b & ~m);
 }
 
 __device__ __forceinline__ std::uint32_t ubfe(std::uint32_t v, std::uint32_t off, std::uint32_t w) {
@@ -119,6 +128,9 @@ struct Console {
     static constexpr std::uint32_t kStride = kFull ? kFullStride : kSplitStride;
     static constexpr std::uint32_t kSpare = kFull ? 2048u : 384u;  // dummy store target
     static constexpr std::uint32_t kRegs = kSpare + 4;              // register area
+    static constexpr std::uint32_t kZp = kFull ? 0u : 0x80u;       // offset of $0000 in the block
+    // Offset of stack byte $0100 + SP - 2 is SP + kStk (SP >= 0x82 in split mode).
+    static constexpr std::uint32_t kStk = kFull ? 0xFEu : static_cast<std::uint32_t>(-0x82);
 
     const DeviceState& s;
     std::uint32_t env, base, pitch;
@@ -150,8 +162,12 @@ struct Console {
     __device__ __forceinline__ static bool ram_in_lds(std::uint32_t ra) {
         return kFull || ((0xBu >> (ra >> 7)) & 1u);  // rows $000-$0FF and $180-$1FF
     }
+    // Block offset of an LDS-resident RAM byte: split mode keeps $0180-$01FF
+    // at 0x000-0x07F and the zero page at 0x080-0x17F, so the offset is one
+    // add and mask; for other rows the result is an in-block byte that is
+    // read and never written.
     __device__ __forceinline__ static std::uint32_t ram_lds_off(std::uint32_t ra) {
-        return kFull ? ra : ra - ((ra >> 1) & 0x80u);
+        return kFull ? (ra & 0x7FFu) : ((ra + 0x80u) & 0x1FFu);
     }
     // Offset of (row, this console) in an address-major interleaved array.
     __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return __umul24(row, pitch) + env; }
@@ -386,9 +402,20 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         const uint4* src = reinterpret_cast<const uint4*>(s.prg_rom);
         uint4* dst = reinterpret_cast<uint4*>(lds);
         for (std::uint32_t i = tid; i < kPrgRomMax / 16; i += T) dst[i] = src[i & (words - 1)];
-        if (tid < 256) reinterpret_cast<uint4*>(lds + kLdsMicro)[tid] = c_micro[tid];
+        // Microcode, with the BRK and NMI vectors (dword 7 of their entries)
+        // taken from the PRG image.
+        const uint4* tab = reinterpret_cast<const uint4*>(kFull ? &c_micro_full : &c_micro_split);
+        const auto vec = [&](std::uint32_t a) {
+            return s.prg_rom[a & s.prg_mask] | (static_cast<std::uint32_t>(s.prg_rom[(a + 1) & s.prg_mask]) << 8);
+        };
+        for (std::uint32_t i = tid; i < mc::kEntries * kMicroBytes / 16; i += T) {
+            uint4 v = tab[i];
+            if (i == 4 * 0x00 + 1) v.w = vec(0x7FFE);
+            if (i == 4 * mc::kNmiEntry + 1) v.w = vec(0x7FFA);
+            reinterpret_cast<uint4*>(lds + kLdsMicro)[i] = v;
+        }
     }
-    const std::uint32_t base = kLdsRam + (lane < L ? slot : 0u) * C::kStride;
+    const std::uint32_t base = kLdsRam + (mine ? slot : (T >> 6) * L) * C::kStride;
     const std::uint32_t P = s.pitch;
     C c{s, mine ? env : 0u, base, P};
     std::uint32_t fd0 = 0, horizon0 = 0;
@@ -403,8 +430,8 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         if (kFull) {
             for (std::uint32_t ra = 0; ra < kRamBytes; ra += 4) stage(ra, ra);
         } else {
-            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) stage(ra, ra);
-            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, ra - 0x80);
+            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) stage(ra, C::ram_lds_off(ra));
+            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, C::ram_lds_off(ra));
         }
         // PPU and pad registers, and the loop state kept off the hot path.
         c.w8(reg::kCtrl, s.ctrl[env]); c.w8(reg::kMask, s.mask[env]); c.w8(reg::kStatus, s.status[env]);
@@ -437,181 +464,114 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
     c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
     c.brk_vec = lds[0x7FFE] | (lds[0x7FFF] << 8);
     std::int32_t left = static_cast<std::int32_t>(horizon0);
-    std::uint32_t in_frame = 0;
-    std::uint64_t instructions = 0;
+    std::uint32_t in_frame = 0, instructions = 0;
     bool active = mine && !(c.flags & kFault) && frameskip != 0;
-    // LDS offset of stack byte $0100 + x (valid for x >= 0x80 in split mode).
-    const std::uint32_t stk = base + (kFull ? 0x100u : 0x80u);
     const std::uint32_t spare = base + C::kSpare;
+    // The next instruction's bytes, fetched as soon as its PC is known.
+    std::uint32_t op, b1, b2;
+    {
+        const std::uint32_t off = c.pc & 0x7FFF;
+        op = lds[off]; b1 = lds[off + 1]; b2 = lds[off + 2];
+    }
 
-    // Every lane runs the datapath each iteration; `active` gates what is
-    // committed (registers, memory writes, I/O, control transfer, timing), so
-    // the loop body has no divergent region around the datapath.
+    // Every lane runs the whole datapath each iteration.  A lane that has
+    // finished its frames runs the NOP entry (changes nothing) and a pending
+    // NMI runs as its own entry, so the commit needs no selects; only memory
+    // and I/O side paths and the rare control cases branch.
+    vmem_settled();  // the state loads above complete before the loop
     while (__ballot(active) != 0) {
-        std::uint32_t dots = 0;
-        // Fetch: opcode and two operand bytes from the PRG image in LDS.
-        std::uint32_t pc0 = c.pc;
-        std::uint32_t off = pc0 & 0x7FFF;
-        std::uint32_t op = lds[off], b1 = lds[off + 1], b2 = lds[off + 2];
-        // Rare: NMI entry before the instruction (cpu.hpp:112-123,
-        // console.hpp:111-115) and code outside PRG ROM (bus reads, in order).
-        if (active && ((c.flags & kNmiPending) || (pc0 - 0x8000u) > 0x7FFDu)) {
-            if (c.flags & kNmiPending) {
-                c.flags &= ~kNmiPending;
-                const std::uint32_t sp = c.regs >> 24;
-                c.ram_wr(0x100 | sp, c.pc >> 8);
-                c.ram_wr(0x100 | ((sp - 1) & 0xFF), c.pc & 0xFF);
-                c.ram_wr(0x100 | ((sp - 2) & 0xFF), (c.p & ~0x10u) | 0x20u);
-                c.regs -= 3u << 24;
-                c.p |= 0x24;
-                c.pc = c.nmi_vec;
-                dots = 21;
-            }
-            pc0 = c.pc;
-            off = pc0 & 0x7FFF;
-            if ((pc0 - 0x8000u) <= 0x7FFDu) {
-                op = lds[off]; b1 = lds[off + 1]; b2 = lds[off + 2];
-            } else {
-                op = c.bus_rd(pc0);
-                const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
-                b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
-                b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
-            }
+        const std::uint32_t pc0 = c.pc, regs0 = c.regs, p0 = c.p;
+        const bool nmi = (c.flags & kNmiPending) != 0;
+        // Rare: code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through
+        // the bus, in order.
+        if (active && !nmi && (pc0 - 0x8000u) > 0x7FFDu) {
+            op = c.bus_rd(pc0);
+            const std::uint32_t len = (lds[kLdsMicro + kMicroBytes * op + 1] >> 4) & 3;  // d0 bits 12-13
+            b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
+            b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
+            vmem_settled();
         }
-        const uint4 m = reinterpret_cast<const uint4*>(lds + kLdsMicro)[op];
-        const std::uint32_t d0 = m.x, d1 = m.y, d2 = m.z, d3 = m.w;
-        const std::uint32_t kind = (d0 >> 10) & 3;
-        // Every conditional below selects between values that are already
-        // computed, so the compiler emits v_cndmask instead of divergent
-        // branches; only memory and I/O side paths branch.
-        // Zero-page pointer of (zp,X) / (zp),Y, from the opcode bits.
-        const std::uint32_t xreg = ubfe(c.regs, 8, 8);
-        const std::uint32_t pidx = ((op & 0x1F) == 0x01) ? xreg : 0u;
-        const std::uint32_t pz = (b1 + pidx) & 0xFF;
-        const std::uint32_t pz1 = (pz + 1) & 0xFF;
-        const std::uint32_t ptr = lds[base + pz] | (lds[base + pz1] << 8);
-        // Effective address.
+        const std::uint32_t mi = active ? (nmi ? mc::kNmiEntry : op) : mc::kNopEntry;
+        const uint4* mw = reinterpret_cast<const uint4*>(lds + kLdsMicro + kMicroBytes * mi);
+        const uint4 ma = mw[0], mb = mw[1], mcw = mw[2], md = mw[3];
+        const std::uint32_t d0 = ma.x, d1 = ma.y, d2 = ma.z, d3 = ma.w;
+        const std::uint32_t d4 = mb.x, d5 = mb.y, d6 = mb.z, d7 = mb.w;
+        const std::uint32_t d8 = mcw.x, d9 = mcw.y, d10 = mcw.z, d11 = mcw.w;
+        const std::uint32_t d12 = md.x, d13 = md.y, d14 = md.z, d15 = md.w;
+
+        // Zero-page pointer of (zp,X) / (zp),Y (opcode bits select X), read
+        // together with the microcode and the stack window.
+        const std::uint32_t xreg = ubfe(regs0, 8, 8);
+        const std::uint32_t pz = (b1 + (((op & 0x1F) == 0x01) ? xreg : 0u)) & 0xFF;
+        const std::uint32_t ptr = lds[base + C::kZp + pz] | (lds[base + C::kZp + ((pz + 1) & 0xFF)] << 8);
+        // Stack window $0100+SP-2 .. $0100+SP+3 (split mode: only when it lies
+        // in the LDS half of the page, else a harmless spare area).
+        const std::uint32_t sp = regs0 >> 24;
+        std::uint32_t wb = base + C::kStk + sp;
+        if (!kFull) wb = sp >= 0x82u ? wb : spare;
+        const std::uint32_t o2 = lds[wb], o1 = lds[wb + 1], o0 = lds[wb + 2];
+        const std::uint32_t w1 = lds[wb + 3], w2 = lds[wb + 4], w3 = lds[wb + 5];
+
+        // Effective address and the operand candidates in LDS.
         const std::uint32_t abs = b1 | (b2 << 8);
         const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
-        const std::uint32_t idx = ubfe(c.regs, d0, d1);
+        const std::uint32_t idx = ubfe(regs0, d0, d1);
         const std::uint32_t ea_full = ebase + idx;
-        const std::uint32_t ea_mask = (d0 & 0x40) ? 0xFFu : 0xFFFFu;
-        const std::uint32_t ea = ea_full & ea_mask;
-        const std::uint32_t cross = (((ebase & 0xFF) + idx) >> 8) & (d0 >> 7) & 1;
-        dots += ((d0 >> 14) & 31) + 3 * cross;
-        // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM
-        // rows, PRG RAM) or the I/O registers.
-        const std::uint32_t ra = ea & 0x7FF;
+        const std::uint32_t ea = ea_full & ((d0 & 0x40) ? 0xFFu : 0xFFFFu);
+        const std::uint32_t cross = ((ea_full ^ ebase) >> 8) & (d0 >> 7) & 1;
+        const std::uint32_t rom_v = lds[ea & 0x7FFF];
+        const std::uint32_t ram_a = base + C::ram_lds_off(ea);
+        const std::uint32_t ram_v = lds[ram_a];
+
+        // Next PC: fall through, branch, absolute (JMP/JSR), pulled return
+        // address (RTS/RTI) or vector (BRK/NMI); its bytes are fetched now.
+        const std::uint32_t fall = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
+        const std::uint32_t taken = ubfe(p0 ^ ((d2 >> 8) & 0xFF), d2, d3);
+        const std::uint32_t target = (fall + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
+        const std::uint32_t bcyc = ((fall ^ target) & 0xFF00) ? 2u : 1u;
+        std::uint32_t next = taken ? target : fall;
+        const std::uint32_t wpull = w1 | (w2 << 8) | (w3 << 16);
+        const std::uint32_t ret_pc = ((wpull >> d12) + ((d12 >> 16) & 1)) & 0xFFFF;
+        next = sel(d9, abs, next);
+        next = sel(d10, ret_pc, next);
+        next = sel(d11, d7, next);
+        std::uint32_t op_n, b1_n, b2_n;
+        {
+            const std::uint32_t off = next & 0x7FFF;
+            op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
+        }
+
+        // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
+        // window contents.
+        const std::uint32_t ret = pc0 + ((d12 >> 24) & 3);
+        const std::uint32_t pb = (p0 & 0xEF) | ((d15 >> 8) & 0xFF);
+        const std::uint32_t pw = __builtin_amdgcn_perm((regs0 << 8) | pb, ret, d5);
+        const std::uint32_t win = sel(d4, pw, o2 | (o1 << 8) | (o0 << 16));
+        const bool stack_side = (sp - ((d13 >> 8) & 0xFF)) > ((d13 >> 16) & 0xFF);
+
+        // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM rows,
+        // PRG RAM), I/O registers, the immediate byte or the pulled byte.
         const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
-        const bool ram_lds = is_ram && C::ram_in_lds(ra);
+        const bool ram_lds = is_ram && C::ram_in_lds(ea & 0x7FF);
         const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
         const bool io = !is_ram && ea < 0x6000;
-        const std::uint32_t rom_off = ea & 0x7FFF;
-        const std::uint32_t ram_off = base + C::ram_lds_off(ra);
-        const std::uint32_t laddr0 = ram_lds ? ram_off : spare;
-        const std::uint32_t laddr = rom ? rom_off : laddr0;
-        const std::uint32_t prgram_row = ea - 0x5800;
-        const std::uint32_t row = is_ram ? ra : prgram_row;
-        const bool rd = d0 & 0x100;
-        const bool wr = (d0 & 0x200) && active;
-        const std::uint32_t ml = lds[laddr];
-        std::uint32_t M = (rd && (rom || ram_lds)) ? ml : b1;
+        const bool rd = d0 & 0x100, wr = d0 & 0x200;
+        const std::uint32_t row = is_ram ? (ea & 0x7FF) : ea - 0x5800;
+        const std::uint32_t m_lds = rom ? rom_v : ram_v;
+        std::uint32_t M = (rd && (rom || ram_lds)) ? m_lds : b1;
+        M = sel(d13, w1, M);
         if (rd && glob) M = s.ram[c.goff(row)];
-        // Work that does not depend on the operand comes first, so the
-        // operand load above is in flight meanwhile.
-        // Next PC: fall through or branch.
-        const std::uint32_t fall = (pc0 + ((d0 >> 12) & 3)) & 0xFFFF;
-        const std::uint32_t taken = ubfe(c.p ^ ((d2 >> 8) & 0xFF), d2, d3);
-        const std::uint32_t target = (fall + static_cast<std::uint32_t>(static_cast<std::int32_t>(static_cast<std::int8_t>(b1)))) & 0xFFFF;
-        const std::uint32_t bdots = ((fall ^ target) & 0xFF00) ? 6u : 3u;
-        const std::uint32_t tdots = taken ? bdots : 0u;
-        dots += tdots;
-        std::uint32_t next = taken ? target : fall;
-        std::uint32_t p_c = c.p, regs_c = c.regs;
-        const bool is_ctrl = kind == mc::KCTRL;
-        if (active && kind == mc::KCTRL) {
-            // Stack and control transfer (cpu.hpp:394-402,603-606,666-694):
-            // JSR/BRK/PHA/PHP push up to 3 bytes at SP, SP-1, SP-2;
-            // RTS/RTI/PLA/PLP pull up to 3 from SP+1..SP+3.
-            const std::uint32_t op_c = (d0 >> 19) & 15;
-            constexpr std::uint32_t kPushes = (2u << (2 * mc::JSR)) | (3u << (2 * mc::BRK)) |
-                                              (1u << (2 * mc::PHA)) | (1u << (2 * mc::PHP));
-            constexpr std::uint32_t kPulls = (2u << (2 * mc::RTS)) | (3u << (2 * mc::RTI)) |
-                                             (1u << (2 * mc::PLA)) | (1u << (2 * mc::PLP));
-            const std::uint32_t npush = (kPushes >> (2 * op_c)) & 3;
-            const std::uint32_t npull = (kPulls >> (2 * op_c)) & 3;
-            const std::uint32_t sp = c.regs >> 24;
-            const std::uint32_t ret = (pc0 + 2) & 0xFFFF;
-            const std::uint32_t pb = c.p | 0x30;
-            const std::uint32_t areg = c.regs & 0xFF, rethi = ret >> 8, retlo = ret & 0xFF;
-            const std::uint32_t v0a = op_c == mc::PHP ? pb : rethi;
-            const std::uint32_t v0 = op_c == mc::PHA ? areg : v0a;
-            std::uint32_t w0, w1, w2;
-            constexpr std::uint32_t kLo = kFull ? 2u : 0x82u;
-            if (sp - kLo <= 0xFCu - kLo) {
-                // The window $01(SP-2)-$01(SP+3) is in LDS without page wrap:
-                // read all six bytes, write back new or old values.
-                const std::uint32_t wb = stk + sp - 2;
-                const std::uint32_t o2 = lds[wb], o1 = lds[wb + 1], o0 = lds[wb + 2];
-                w0 = lds[wb + 3]; w1 = lds[wb + 4]; w2 = lds[wb + 5];
-                const std::uint32_t n0 = npush >= 1 ? v0 : o0;
-                const std::uint32_t n1 = npush >= 2 ? retlo : o1;
-                const std::uint32_t n2 = npush >= 3 ? pb : o2;
-                lds[wb + 2] = static_cast<std::uint8_t>(n0);
-                lds[wb + 1] = static_cast<std::uint8_t>(n1);
-                lds[wb] = static_cast<std::uint8_t>(n2);
-            } else {
-                if (npush >= 1) c.ram_wr(0x100 | sp, v0);
-                if (npush >= 2) c.ram_wr(0x100 | ((sp - 1) & 0xFF), retlo);
-                if (npush >= 3) c.ram_wr(0x100 | ((sp - 2) & 0xFF), pb);
-                w0 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
-                w1 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
-                w2 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
-            }
-            const std::uint32_t nsp = (sp - npush + npull) & 0xFF;
-            regs_c = (c.regs & 0x00FFFFFFu) | (nsp << 24);
-            const std::uint32_t pulled_p = (w0 | 0x20) & ~0x10u;
-            const std::uint32_t brk_p = c.p | 0x24;
-            const std::uint32_t p_b = op_c == mc::BRK ? brk_p : c.p;
-            p_c = (op_c == mc::RTI || op_c == mc::PLP) ? pulled_p : p_b;
-            if (op_c == mc::PLA) {
-                regs_c = (regs_c & ~0xFFu) | w0;
-                p_c = (p_c & 0x7D) | (w0 & 0x80) | (w0 == 0 ? 2u : 0u) | 0x20;
-            }
-            const std::uint32_t rts_pc = ((w0 | (w1 << 8)) + 1) & 0xFFFF, rti_pc = w1 | (w2 << 8);
-            const std::uint32_t n3 = op_c == mc::BRK ? c.brk_vec : next;
-            const std::uint32_t n2 = op_c == mc::RTI ? rti_pc : n3;
-            const std::uint32_t n1 = op_c == mc::RTS ? rts_pc : n2;
-            next = (op_c == mc::JMPA || op_c == mc::JSR) ? abs : n1;
-            if (op_c == mc::JMPI) {  // JMP ($xxxx) with the page-wrap fetch
-                const std::uint32_t l = c.bus_rd(abs);
-                next = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
-            }
-            // Idle loop (JMP to itself): the console repeats 3-cycle jumps
-            // until the next timing event; account for them in one go.
-            const std::int32_t gap = left - static_cast<std::int32_t>(dots);
-            if (op_c == mc::JMPA && abs == pc0 && gap > 0) {
-                std::int32_t k = (gap + 8) / 9;
-                if (kBudget) {
-                    const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame) - 1;
-                    k = k < room ? k : room;
-                }
-                dots += 9u * static_cast<std::uint32_t>(k);
-                in_frame += static_cast<std::uint32_t>(k);
-                instructions += static_cast<std::uint64_t>(k);
-                if constexpr (kStats == 2) {
-                    atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
-                    atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
-                }
-            }
+        if (rd && io) {
+            M = c.io_rd(ea);
+            vmem_settled();
         }
-        if (rd && io && active) M = c.io_rd(ea);
+
         // Adder, logic unit and right shifter.
-        const std::uint32_t R = ubfe(c.regs, d2, 8);
+        const std::uint32_t R = ubfe(regs0, d2, 8);
         const std::uint32_t xa = (d1 & 0x20) ? M : R;
         const std::uint32_t bsrc = (d1 & 0x40) ? xa : M;
         const std::uint32_t xb = (bsrc & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
-        const std::uint32_t cf = c.p & 1;
+        const std::uint32_t cf = p0 & 1;
         const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
         const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
         const bool right = d1 & 0x200;
@@ -625,38 +585,95 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
         const std::uint32_t f = nv | (r == 0 ? 2u : 0u) | carry;
         const std::uint32_t fm = d0 >> 24;
-        const std::uint32_t p1 = (c.p & ~fm) | (f & fm);
-        const std::uint32_t pn = (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
-        // Register write-back (a control opcode's own results win).
-        const std::uint32_t doff = (d3 >> 5) & 31, dmask = ((1u << ((d3 >> 10) & 31)) - 1u) << doff;
-        const std::uint32_t regs_n = (c.regs & ~dmask) | ((r << doff) & dmask);
-        // Memory write: LDS RAM (non-writers store to their spare byte), HBM
-        // (non-writers store to their trash byte), or an I/O register.
-        const std::uint32_t waddr = (wr && ram_lds) ? laddr : spare;
+        const std::uint32_t p1 = (p0 & ~fm) | (f & fm);
+        const std::uint32_t pn = sel(d15, (M & 0xCF) | 0x20, (p1 & ((d3 >> 16) & 0xFF)) | (d3 >> 24));
+        const std::uint32_t regs_n = sel(d8, r << ((d3 >> 5) & 31), regs0) + d6;
+
+        // Memory writes: the stack window (pushed or old bytes), then the
+        // operand to LDS (non-writers store to their spare byte).
+        lds[wb] = static_cast<std::uint8_t>(win);
+        lds[wb + 1] = static_cast<std::uint8_t>(win >> 8);
+        lds[wb + 2] = static_cast<std::uint8_t>(win >> 16);
+        const std::uint32_t waddr = (wr && ram_lds) ? ram_a : spare;
         lds[waddr] = static_cast<std::uint8_t>(r);
-        if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
-        if (wr && io) dots += c.io_wr(ea, r);
-        p_c = is_ctrl ? p_c : pn;
-        regs_c = is_ctrl ? regs_c : regs_n;
-        // Commit (an illegal opcode freezes the console before it executes).
-        const bool legal = kind != mc::KILLEGAL;
-        const bool commit = active && legal;
-        c.pc = commit ? next : c.pc;
-        c.regs = commit ? regs_c : c.regs;
-        c.p = commit ? p_c : c.p;
-        c.flags |= (active && !legal) ? kFault : 0u;
-        const std::uint32_t counted = commit ? 1u : 0u;
+
+        // Commit.  The NOP entry leaves everything as it was.
+        c.pc = next;
+        c.regs = regs_n;
+        c.p = pn;
+        c.flags &= ~((d14 >> 1) & kNmiPending);
+        op = op_n; b1 = b1_n; b2 = b2_n;
+        std::uint32_t dots = 3 * (((d0 >> 14) & 31) + cross + (taken ? bcyc : 0u));
+        const std::uint32_t counted = d14 & mc::kCount;
         in_frame += counted;
         instructions += counted;
         if constexpr (kStats == 2) {
-            if (commit) {
-                atomicAdd(&s.prof_opcodes[op], 1ull);
+            if (counted) {
+                atomicAdd(&s.prof_opcodes[mi], 1ull);
                 atomicAdd(&s.prof_pcs[pc0], 1ull);
             }
         }
-        active = commit;
-        left -= commit ? static_cast<std::int32_t>(dots) : 0;
-        if (active && left <= 0) {  // a timing event was crossed: settle the PPU
+        if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
+        if (wr && io) dots += c.io_wr(ea, r);
+
+        // Rare control cases, redone from the instruction's starting state:
+        // JMP ($xxxx) with the page-wrap pointer fetch, and stack opcodes
+        // whose bytes leave the LDS window (bus-level RAM accesses).
+        if ((d14 & mc::kJmpInd) || stack_side) {
+            std::uint32_t npc = next;
+            if (d14 & mc::kJmpInd) {
+                const std::uint32_t l = c.bus_rd(abs);
+                npc = l | (c.bus_rd((abs & 0xFF00) | ((abs + 1) & 0xFF)) << 8);
+            } else {
+                const std::uint32_t npush = (d4 >> 16 & 1) + (d4 >> 8 & 1) + (d4 & 1);
+                for (std::uint32_t k = 0; k < npush; ++k)
+                    c.ram_wr(0x100 | ((sp - k) & 0xFF), (pw >> (8 * (2 - k))) & 0xFF);
+                const std::uint32_t v1 = c.ram_rd(0x100 | ((sp + 1) & 0xFF));
+                const std::uint32_t v2 = c.ram_rd(0x100 | ((sp + 2) & 0xFF));
+                const std::uint32_t v3 = c.ram_rd(0x100 | ((sp + 3) & 0xFF));
+                const std::uint32_t vp = v1 | (v2 << 8) | (v3 << 16);
+                const std::uint32_t vret = ((vp >> d12) + ((d12 >> 16) & 1)) & 0xFFFF;
+                npc = sel(d10, vret, next);
+                // PLA: A = pulled byte with N and Z; PLP / RTI: P = pulled byte.
+                const std::uint32_t pa = (p0 & ((d3 >> 16) & 0xFF)) | (d3 >> 24);
+                std::uint32_t np = sel(d15, (v1 & 0xCF) | 0x20, pa);
+                std::uint32_t nregs = regs0 + d6;
+                if (d8 & 0xFF) {
+                    nregs = (nregs & ~0xFFu) | v1;
+                    np = (np & 0x7D) | (v1 & 0x80) | (v1 == 0 ? 2u : 0u);
+                }
+                c.regs = nregs;
+                c.p = np;
+            }
+            vmem_settled();
+            c.pc = npc;
+            const std::uint32_t off = npc & 0x7FFF;
+            op = lds[off]; b1 = lds[off + 1]; b2 = lds[off + 2];
+        }
+        // Idle loop (JMP to itself): the console repeats 3-cycle jumps until
+        // the next timing event; account for them in one go.
+        const std::int32_t gap = left - static_cast<std::int32_t>(dots);
+        if ((d14 & mc::kJmpAbs) && abs == pc0 && gap > 0) {
+            std::int32_t k = (gap + 8) / 9;
+            if (kBudget) {
+                const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame);
+                k = k < room ? k : room;
+            }
+            dots += 9u * static_cast<std::uint32_t>(k);
+            in_frame += static_cast<std::uint32_t>(k);
+            instructions += static_cast<std::uint32_t>(k);
+            if constexpr (kStats == 2) {
+                atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
+                atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
+            }
+        }
+        // An illegal opcode freezes the console (the NOP-like entry changed nothing).
+        if (d14 & mc::kIllegal) {
+            c.flags |= kFault;
+            active = false;
+        }
+        left -= static_cast<std::int32_t>(dots);
+        if (counted && left <= 0) {  // a timing event was crossed: settle the PPU
             const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
             const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
             c.w32(reg::kHorizon, h);
@@ -669,7 +686,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
                 if (fl == 0) active = false;
             }
         }
-        if (kBudget && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
+        if (kBudget && counted && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
             const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
             const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
             c.w32(reg::kHorizon, h);
@@ -744,8 +761,8 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         if (kFull) {
             for (std::uint32_t ra = 0; ra < kRamBytes; ra += 4) unstage(ra, ra);
         } else {
-            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) unstage(ra, ra);
-            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) unstage(ra, ra - 0x80);
+            for (std::uint32_t ra = 0; ra < 0x100; ra += 4) unstage(ra, C::ram_lds_off(ra));
+            for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) unstage(ra, C::ram_lds_off(ra));
         }
     }
     const std::uint32_t fd = c.r32(reg::kFrameDot);
