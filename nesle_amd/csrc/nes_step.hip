@@ -51,7 +51,11 @@ __constant__ mc::Table c_micro_full = mc::kTableFull;
 extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
 
 constexpr std::uint32_t kMaxBlock = 1024;       // up to 16 waves per workgroup
-constexpr std::uint32_t kMicroBytes = 4 * mc::kDwords;                 // 64 B per entry
+// Microcode in LDS as four tables of 16-byte quarters (dwords 0-3, 4-7, 8-11,
+// 12-15 of every entry): lanes reading different entries then spread over the
+// banks as with 16-byte entries, where 64-byte entries would pile onto few.
+constexpr std::uint32_t kMicroBytes = 4 * mc::kDwords;                   // 64 B per entry
+constexpr std::uint32_t kMicroQuarter = 16 * mc::kEntries;               // bytes per table
 constexpr std::uint32_t kLdsMicro = 32768;                               // after the PRG image
 constexpr std::uint32_t kLdsRam = kLdsMicro + mc::kEntries * kMicroBytes; // console RAM blocks
 // Per-console LDS block: RAM rows, 4 spare bytes, then a 40-byte register
@@ -412,7 +416,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
             uint4 v = tab[i];
             if (i == 4 * 0x00 + 1) v.w = vec(0x7FFE);
             if (i == 4 * mc::kNmiEntry + 1) v.w = vec(0x7FFA);
-            reinterpret_cast<uint4*>(lds + kLdsMicro)[i] = v;
+            reinterpret_cast<uint4*>(lds + kLdsMicro + (i & 3) * kMicroQuarter)[i >> 2] = v;
         }
     }
     const std::uint32_t base = kLdsRam + (mine ? slot : (T >> 6) * L) * C::kStride;
@@ -486,14 +490,17 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         // the bus, in order.
         if (active && !nmi && (pc0 - 0x8000u) > 0x7FFDu) {
             op = c.bus_rd(pc0);
-            const std::uint32_t len = (lds[kLdsMicro + kMicroBytes * op + 1] >> 4) & 3;  // d0 bits 12-13
+            const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
             b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
             b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
             vmem_settled();
         }
         const std::uint32_t mi = active ? (nmi ? mc::kNmiEntry : op) : mc::kNopEntry;
-        const uint4* mw = reinterpret_cast<const uint4*>(lds + kLdsMicro + kMicroBytes * mi);
-        const uint4 ma = mw[0], mb = mw[1], mcw = mw[2], md = mw[3];
+        const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
+        const uint4 ma = *reinterpret_cast<const uint4*>(mw);
+        const uint4 mb = *reinterpret_cast<const uint4*>(mw + kMicroQuarter);
+        const uint4 mcw = *reinterpret_cast<const uint4*>(mw + 2 * kMicroQuarter);
+        const uint4 md = *reinterpret_cast<const uint4*>(mw + 3 * kMicroQuarter);
         const std::uint32_t d0 = ma.x, d1 = ma.y, d2 = ma.z, d3 = ma.w;
         const std::uint32_t d4 = mb.x, d5 = mb.y, d6 = mb.z, d7 = mb.w;
         const std::uint32_t d8 = mcw.x, d9 = mcw.y, d10 = mcw.z, d11 = mcw.w;
