@@ -48,7 +48,10 @@ namespace {
 __constant__ mc::Table c_micro_split = mc::kTableSplit;
 __constant__ mc::Table c_micro_full = mc::kTableFull;
 
-extern __shared__ __attribute__((aligned(16))) std::uint8_t lds[];
+// The whole 160 KB of a CU's LDS, statically: one workgroup per CU, and a
+// static array has a known address (0), so LDS addresses need no base add.
+constexpr std::uint32_t kLdsLimit = 160u * 1024u;
+__shared__ __attribute__((aligned(16))) std::uint8_t lds[kLdsLimit];
 
 constexpr std::uint32_t kMaxBlock = 1024;       // up to 16 waves per workgroup
 // Microcode in LDS as four tables of 16-byte quarters (dwords 0-3, 4-7, 8-11,
@@ -78,7 +81,6 @@ constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4;
 // Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
 // write to (one spare byte per console after PRG RAM).
 constexpr std::uint32_t kTrashRow = kRamBytes + kPrgRamBytes;
-constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 
 // Lanes without a console run the datapath on a dummy block after the last
 // console's (they write only their own stack window and spare byte).  The
@@ -107,6 +109,11 @@ __device__ __forceinline__ void vmem_settled() { __builtin_amdgcn_s_waitcnt(0x0F
 __device__ __forceinline__ std::uint32_t sel(std::uint32_t m, std::uint32_t a, std::uint32_t b) {
     return (a & m) | (b & ~m);
 }
+
+// Instruction bytes are carried across iterations as 32-bit values already
+// zero-extended by the LDS byte read; hiding them from the optimizer keeps it
+// from narrowing the loop-carried value to 8 bits and re-extending it.
+__device__ __forceinline__ void opaque(std::uint32_t& v) { asm("" : "+v"(v)); }
 
 __device__ __forceinline__ std::uint32_t ubfe(std::uint32_t v, std::uint32_t off, std::uint32_t w) {
     return __builtin_amdgcn_ubfe(v, off, w);
@@ -356,7 +363,7 @@ struct Console {
         if (addr < 0x2000) return ram_rd(addr & 0x7FF);
         if (addr >= 0x8000) return lds[addr & 0x7FFF];
         if (addr >= 0x6000) return s.ram[goff(addr - 0x5800)];
-        return io_rd(addr);
+        return io_rd(addr) & 0xFF;
     }
 
     // ---- PPU timing (ppu.hpp:46-76) -------------------------------------------------
@@ -546,6 +553,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         {
             const std::uint32_t off = next & 0x7FFF;
             op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
+            opaque(op_n); opaque(b1_n); opaque(b2_n);
         }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
@@ -846,10 +854,7 @@ Geometry geometry(std::uint32_t n, std::uint32_t waves) {
 template <int kStats, bool kFull, bool kBudget>
 hipError_t launch_variant(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
                           std::uint32_t auto_reset, hipStream_t stream) {
-    const void* fn = reinterpret_cast<const void*>(&step_kernel<kStats, kFull, kBudget>);
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(g.lds));
-    if (e != hipSuccess) return e;
-    step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(64 * g.waves), g.lds, stream>>>(
+    step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(64 * g.waves), 0, stream>>>(
         s, frameskip, max_instr, auto_reset, g.lane_bits);
     return hipGetLastError();
 }
