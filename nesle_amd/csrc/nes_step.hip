@@ -484,6 +484,16 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         const std::uint32_t off = c.pc & 0x7FFF;
         op = lds[off]; b1 = lds[off + 1]; b2 = lds[off + 2];
     }
+    // Code outside PRG ROM: the bytes come through the bus, in order.
+    auto fetch_bus = [&]() {
+        const std::uint32_t pc = c.pc;
+        op = c.bus_rd(pc);
+        const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
+        b1 = len >= 2 ? c.bus_rd((pc + 1) & 0xFFFF) : 0u;
+        b2 = len >= 3 ? c.bus_rd((pc + 2) & 0xFFFF) : 0u;
+        vmem_settled();
+    };
+    if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
 
     // Every lane runs the whole datapath each iteration.  A lane that has
     // finished its frames runs the NOP entry (changes nothing) and a pending
@@ -493,15 +503,6 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
     while (__ballot(active) != 0) {
         const std::uint32_t pc0 = c.pc, regs0 = c.regs, p0 = c.p;
         const bool nmi = (c.flags & kNmiPending) != 0;
-        // Rare: code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through
-        // the bus, in order.
-        if (active && !nmi && (pc0 - 0x8000u) > 0x7FFDu) {
-            op = c.bus_rd(pc0);
-            const std::uint32_t len = (lds[kLdsMicro + 16 * op + 1] >> 4) & 3;  // d0 bits 12-13
-            b1 = len >= 2 ? c.bus_rd((pc0 + 1) & 0xFFFF) : 0u;
-            b2 = len >= 3 ? c.bus_rd((pc0 + 2) & 0xFFFF) : 0u;
-            vmem_settled();
-        }
         const std::uint32_t mi = active ? (nmi ? mc::kNmiEntry : op) : mc::kNopEntry;
         const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
         const uint4 ma = *reinterpret_cast<const uint4*>(mw);
@@ -629,12 +630,23 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
             }
         }
         if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
-        if (wr && io) dots += c.io_wr(ea, r);
-
-        // Rare control cases, redone from the instruction's starting state:
-        // JMP ($xxxx) with the page-wrap pointer fetch, and stack opcodes
-        // whose bytes leave the LDS window (bus-level RAM accesses).
-        if ((d14 & mc::kJmpInd) || stack_side) {
+        // Rare work, tested once per iteration: I/O register writes, JMP
+        // ($xxxx), stack bytes outside the LDS window, the idle loop, illegal
+        // opcodes, PPU timing events, the frame budget, OAM DMA and code
+        // outside PRG ROM.
+        const bool io_write = wr && io;
+        const bool side = (d14 & mc::kJmpInd) || stack_side;
+        const bool idle = (d14 & mc::kJmpAbs) && abs == pc0;
+        const bool timing = counted && (left - static_cast<std::int32_t>(dots)) <= 0;
+        const bool budget = kBudget && counted && in_frame >= max_instr;
+        const bool rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
+                          (next - 0x8000u) > 0x7FFDu;
+        if (__ballot(rare) == 0) {
+            left -= static_cast<std::int32_t>(dots);
+            continue;
+        }
+        if (io_write) dots += c.io_wr(ea, r);
+        if (side) {
             std::uint32_t npc = next;
             if (d14 & mc::kJmpInd) {
                 const std::uint32_t l = c.bus_rd(abs);
@@ -668,7 +680,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         // Idle loop (JMP to itself): the console repeats 3-cycle jumps until
         // the next timing event; account for them in one go.
         const std::int32_t gap = left - static_cast<std::int32_t>(dots);
-        if ((d14 & mc::kJmpAbs) && abs == pc0 && gap > 0) {
+        if (idle && gap > 0) {
             std::int32_t k = (gap + 8) / 9;
             if (kBudget) {
                 const std::int32_t room = static_cast<std::int32_t>(max_instr) - static_cast<std::int32_t>(in_frame);
@@ -754,6 +766,9 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
             }
         }
         c.flags &= ~kDmaPending;
+        // Code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through the bus,
+        // in order, once the PPU has settled.
+        if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
     }
 
     if (!mine) return;
