@@ -1,6 +1,6 @@
 // nes_micro.h -- the 6502 microcode of the step kernel (nes_step.hip).
 //
-// One 64-byte word (sixteen dwords d[0..15]) per opcode drives a single
+// One 80-byte word (twenty dwords d[0..19]) per opcode drives a single
 // branch-free datapath: effective address, operand, an adder / logic unit /
 // right shifter, flag merge, register write-back, a three-byte stack window
 // (pushes, pulls, stack-pointer change) and the next-PC selection.  Besides
@@ -59,6 +59,12 @@
 //       2 JMP absolute (idle-loop check), 3 JMP indirect (side path),
 //       4 illegal opcode
 //   d15 0-7 P := pulled byte (PLP, RTI), 8-15 B/U bits of a pushed P
+//   d16 0-15 base is the zero-page pointer (0xFFFF or 0); 16-23 base CPU
+//       cycles
+//   d17 effective-address mask (0xFF zero page, 0xFFFF otherwise)
+//   d18 0-7 adder input A is the operand M (0xFF or 0); 8 carry in = C flag;
+//       16 carry in 1
+//   d19 0-7 unit: right shifter (0xFF or 0)
 #pragma once
 
 #include <cstdint>
@@ -66,7 +72,7 @@
 namespace nesle {
 namespace mc {
 
-constexpr std::uint32_t kDwords = 16;
+constexpr std::uint32_t kDwords = 20;
 constexpr std::uint32_t kNopEntry = 256, kNmiEntry = 257, kEntries = 258;
 // d14 bits.
 constexpr std::uint32_t kCount = 1, kClearNmi = 2, kJmpAbs = 4, kJmpInd = 8, kIllegal = 16;
@@ -123,6 +129,9 @@ constexpr Word base(std::uint32_t mode, std::uint32_t cycles, bool penalty) {
     w.set(0, 12, 2, mode_len(mode));
     w.set(0, 14, 5, cycles);
     w.set(14, 0, 5, kCount);
+    w.set(16, 0, 16, (mode == INDX || mode == INDY) ? 0xFFFFu : 0u);
+    w.set(16, 16, 8, cycles);
+    w.set(17, 0, 32, (mode == ZP || mode == ZPX || mode == ZPY) ? 0xFFu : 0xFFFFu);
     return w;
 }
 
@@ -137,6 +146,9 @@ constexpr Word adder(Word w, bool a_is_m, std::uint32_t reg, bool b_from_a, std:
     w.set(1, 7, 1, cin_1 ? 1u : 0u);
     w.set(1, 8, 1, cin_c ? 1u : 0u);
     w.set(2, 24, 8, 0xFF);
+    w.set(18, 0, 8, a_is_m ? 0xFFu : 0u);
+    w.set(18, 8, 1, cin_c ? 1u : 0u);
+    w.set(18, 16, 1, cin_1 ? 1u : 0u);
     return w;
 }
 
@@ -207,6 +219,8 @@ constexpr Word shift(std::uint32_t mode, std::uint32_t cyc, bool right, bool rot
         w.set(2, 0, 5, 0);
         w.set(1, 9, 1, 1);
         w.set(1, 10, 1, rot ? 1u : 0u);
+        w.set(18, 0, 8, mem ? 0xFFu : 0u);
+        w.set(19, 0, 8, 0xFF);
     } else {
         w = adder(w, mem, RA, true, 0xFF, 0, false, rot);
     }

@@ -54,10 +54,11 @@ constexpr std::uint32_t kLdsLimit = 160u * 1024u;
 __shared__ __attribute__((aligned(16))) std::uint8_t lds[kLdsLimit];
 
 constexpr std::uint32_t kMaxBlock = 1024;       // up to 16 waves per workgroup
-// Microcode in LDS as four tables of 16-byte quarters (dwords 0-3, 4-7, 8-11,
-// 12-15 of every entry): lanes reading different entries then spread over the
-// banks as with 16-byte entries, where 64-byte entries would pile onto few.
-constexpr std::uint32_t kMicroBytes = 4 * mc::kDwords;                   // 64 B per entry
+// Microcode in LDS as five tables of 16-byte slices (dwords 0-3, 4-7, ...,
+// 16-19 of every entry): lanes reading different entries then spread over the
+// banks as with 16-byte entries, where 80-byte entries would pile onto few.
+constexpr std::uint32_t kMicroBytes = 4 * mc::kDwords;                   // 80 B per entry
+constexpr std::uint32_t kMicroSlices = mc::kDwords / 4;
 constexpr std::uint32_t kMicroQuarter = 16 * mc::kEntries;               // bytes per table
 constexpr std::uint32_t kLdsMicro = 32768;                               // after the PRG image
 constexpr std::uint32_t kLdsRam = kLdsMicro + mc::kEntries * kMicroBytes; // console RAM blocks
@@ -421,9 +422,9 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         };
         for (std::uint32_t i = tid; i < mc::kEntries * kMicroBytes / 16; i += T) {
             uint4 v = tab[i];
-            if (i == 4 * 0x00 + 1) v.w = vec(0x7FFE);
-            if (i == 4 * mc::kNmiEntry + 1) v.w = vec(0x7FFA);
-            reinterpret_cast<uint4*>(lds + kLdsMicro + (i & 3) * kMicroQuarter)[i >> 2] = v;
+            if (i == kMicroSlices * 0x00 + 1) v.w = vec(0x7FFE);
+            if (i == kMicroSlices * mc::kNmiEntry + 1) v.w = vec(0x7FFA);
+            reinterpret_cast<uint4*>(lds + kLdsMicro + (i % kMicroSlices) * kMicroQuarter)[i / kMicroSlices] = v;
         }
     }
     const std::uint32_t base = kLdsRam + (mine ? slot : (T >> 6) * L) * C::kStride;
@@ -509,10 +510,12 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         const uint4 mb = *reinterpret_cast<const uint4*>(mw + kMicroQuarter);
         const uint4 mcw = *reinterpret_cast<const uint4*>(mw + 2 * kMicroQuarter);
         const uint4 md = *reinterpret_cast<const uint4*>(mw + 3 * kMicroQuarter);
+        const uint4 me = *reinterpret_cast<const uint4*>(mw + 4 * kMicroQuarter);
         const std::uint32_t d0 = ma.x, d1 = ma.y, d2 = ma.z, d3 = ma.w;
         const std::uint32_t d4 = mb.x, d5 = mb.y, d6 = mb.z, d7 = mb.w;
         const std::uint32_t d8 = mcw.x, d9 = mcw.y, d10 = mcw.z, d11 = mcw.w;
         const std::uint32_t d12 = md.x, d13 = md.y, d14 = md.z, d15 = md.w;
+        const std::uint32_t d16 = me.x, d17 = me.y, d18 = me.z, d19 = me.w;
 
         // Zero-page pointer of (zp,X) / (zp),Y (opcode bits select X), read
         // together with the microcode and the stack window.
@@ -529,10 +532,10 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
 
         // Effective address and the operand candidates in LDS.
         const std::uint32_t abs = b1 | (b2 << 8);
-        const std::uint32_t ebase = (d0 & 0x20) ? ptr : abs;
+        const std::uint32_t ebase = sel(d16, ptr, abs);
         const std::uint32_t idx = ubfe(regs0, d0, d1);
         const std::uint32_t ea_full = ebase + idx;
-        const std::uint32_t ea = ea_full & ((d0 & 0x40) ? 0xFFu : 0xFFFFu);
+        const std::uint32_t ea = ea_full & d17;
         const std::uint32_t cross = ((ea_full ^ ebase) >> 8) & (d0 >> 7) & 1;
         const std::uint32_t rom_v = lds[ea & 0x7FFF];
         const std::uint32_t ram_a = base + C::ram_lds_off(ea);
@@ -584,18 +587,16 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
 
         // Adder, logic unit and right shifter.
         const std::uint32_t R = ubfe(regs0, d2, 8);
-        const std::uint32_t xa = (d1 & 0x20) ? M : R;
+        const std::uint32_t xa = sel(d18, M, R);
         const std::uint32_t bsrc = (d1 & 0x40) ? xa : M;
         const std::uint32_t xb = (bsrc & ((d1 >> 16) & 0xFF)) ^ (d1 >> 24);
         const std::uint32_t cf = p0 & 1;
-        const std::uint32_t sum = xa + xb + (((d1 >> 7) & 1) | (cf & (d1 >> 8)));
+        const std::uint32_t sum = xa + xb + ((cf & (d18 >> 8)) | ((d18 >> 16) & 1));
         const std::uint32_t lres = (R & M & ((d2 >> 8) & 0xFF)) | ((R ^ M) & ((d2 >> 16) & 0xFF));
-        const bool right = d1 & 0x200;
         const std::uint32_t sr = (xa >> 1) | ((cf & (d1 >> 10)) << 7);
         const std::uint32_t ar = (sum & (d2 >> 24)) | lres;
-        const std::uint32_t r = right ? sr : ar;
-        const std::uint32_t c_right = xa & 1, c_add = (sum >> 8) & 1;
-        const std::uint32_t carry = right ? c_right : c_add;
+        const std::uint32_t r = sel(d19, sr, ar);
+        const std::uint32_t carry = sel(d19, xa, sum >> 8) & 1;
         const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
         const std::uint32_t nv_bit = M & 0xC0, nv_alu = (r & 0x80) | ovf;
         const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
@@ -619,7 +620,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         c.p = pn;
         c.flags &= ~((d14 >> 1) & kNmiPending);
         op = op_n; b1 = b1_n; b2 = b2_n;
-        std::uint32_t dots = 3 * (((d0 >> 14) & 31) + cross + (taken ? bcyc : 0u));
+        std::uint32_t dots = 3 * ((d16 >> 16) + cross + (taken ? bcyc : 0u));
         const std::uint32_t counted = d14 & mc::kCount;
         in_frame += counted;
         instructions += counted;
