@@ -17,9 +17,12 @@ the whole action table) are resident in HBM before timing starts.
 Roofline: the step kernel's launches are timed with HIP events on the stream
 it runs on.  ``roofline`` prices the algorithmic HBM bytes per env-step
 (RAM read+write 4,096 + OAM read+write 512 + registers/PPU/reward scalars 128
-+ action 1 + reward/done 5 = 4,742 B) against 8 TB/s; ``roofline_valu``
-prices the emulated 6502 instruction rate against the integer-VALU issue
-peak (256 CUs x 4 SIMD x 16 lanes x 2.4 GHz).
++ action 1 + reward/done 5 = 4,742 B) against 8 TB/s; its ``traffic`` is the
+HBM bytes per launch that rocprofv3 measured (FETCH_SIZE and WRITE_SIZE,
+scaled by a copy-kernel calibration) in profiles/step_kernel_65536_fs4.md.
+``roofline_valu`` gives the emulated 6502 instruction rate and the VALU pipe
+busy fraction from the same profile (SQ_INSTS_VALU x 4 cycles over 1,024
+SIMDs and the kernel time).
 
 ``cpu_baseline``: the reference's own CPU core (``nesle::Console`` compiled
 from the reference sources into oracle/_ref) on the host's cores, one console
@@ -50,6 +53,21 @@ TIME_PENALTY = 0.01
 B_STEP = 4742                       # algorithmic HBM bytes per env-step
 HBM_PEAK_GBS = 8000.0
 VALU_PEAK_LANE_OPS = 256 * 4 * 16 * 2.4e9   # int32 lane-ops/s
+
+
+PROFILE = ROOT / "profiles" / "step_kernel_65536_fs4.md"
+
+
+def profile_figure(key: str, num_envs: int) -> float | None:
+    """A machine-readable figure (``<key> <envs> <value>``) of the committed
+    rocprofv3 summary, or None when the summary has none for this size."""
+    if not PROFILE.exists():
+        return None
+    for line in PROFILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == key and parts[1] == str(num_envs):
+            return float(parts[2])
+    return None
 
 
 def log(msg: str) -> None:
@@ -250,11 +268,15 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": hbm_achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": profile_figure("traffic_bytes_per_launch", args.envs),
+            "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000, profiles/step_kernel_65536_fs4.md",
         },
         "roofline_valu": {
             "achieved_emulated_instr_per_s": instr_rate,
             "instructions_per_env_step": big["instructions_per_env_step"],
+            "valu_busy_frac": profile_figure("valu_busy", args.envs),
+            "valu_busy_source": "rocprofv3 SQ_INSTS_VALU x 4 cycles / (1,024 SIMDs x kernel time), "
+                                "profiles/step_kernel_65536_fs4.md",
             "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
         },

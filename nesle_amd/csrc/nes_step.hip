@@ -15,19 +15,19 @@
 // round trips on that path.  Hence:
 //  * Geometry: 4 waves per workgroup, L = N/1024 (rounded up to a power of
 //    two, at most 64) consoles per wave, so every SIMD holds one wave however
-//    small the batch.  Small batches thus get few, short waves (less
-//    divergence) instead of a few full waves on a few CUs.
-//  * LDS holds the PRG ROM (32 KB), the 128-bit microcode table and console
-//    RAM: all 2 KB of it when 4L consoles fit (L <= 8), otherwise the zero page
-//    and $0180-$01FF.  Each console's RAM is one contiguous LDS block whose
-//    stride is 1 dword modulo the bank count, so lanes at equal addresses hit
-//    distinct banks.  Remaining RAM rows and PRG RAM are address-major
-//    interleaved in HBM (row * pitch + env): lanes at equal addresses coalesce.
-//  * Registers A/X/Y/SP are packed in one VGPR and read/written with bitfield
-//    extract/insert driven by the microcode (nes_micro.h).  Every PPU and pad
-//    register lives in a VGPR for the whole launch.
-//  * The datapath is branch-free; stack/control opcodes, I/O registers, NMI
-//    entry and PPU settlement take divergent side paths.
+//    small the batch.
+//  * LDS (a static 160 KB array) holds the PRG ROM (32 KB), the microcode
+//    (nes_micro.h) and console RAM: all 2 KB of it when 4L consoles fit
+//    (L <= 8), otherwise the zero page and $0180-$01FF.  Other RAM rows and
+//    PRG RAM are address-major interleaved in HBM (row * pitch + env).
+//  * Registers A/X/Y/SP are packed in one VGPR; the microcode drives one
+//    branch-free datapath (addressing, stack window, next PC, ALU, flags).
+//    Finished lanes and NMI entry run as virtual opcodes, so nothing needs a
+//    commit select.  PPU and pad registers live in a per-console LDS area.
+//  * Only the HBM operand and the I/O register read branch inside the loop;
+//    everything rare (I/O writes, JMP indirect, stack wrap, idle loops,
+//    illegal opcodes, PPU events, OAM DMA, code outside ROM) sits behind one
+//    wave-uniform test.
 //  * OAM DMA is done by the whole wave for one console at a time (4 bytes per
 //    lane) instead of a 256-iteration loop in one lane.
 //  * The CPU cycle counter is not updated per instruction: every cycle is 3
