@@ -52,7 +52,17 @@ enum {
     NESLE_VIEW_OPCODES = 7,      /* uint64 [256]     (after profile steps)  */
     NESLE_VIEW_PCS = 8,          /* uint64 [65536]                          */
     NESLE_VIEW_OAM = 9,          /* uint8  [num_envs][256] (host copy only) */
-    NESLE_VIEW_COUNT = 10
+    NESLE_VIEW_FRAME_RGB = 10,   /* uint8  [num_envs][240][256][3] (after nesle_render) */
+    NESLE_VIEW_FRAME_PALETTE = 11, /* uint8 [num_envs][240][256] palette values 0-63 */
+    NESLE_VIEW_GRAY84 = 12,      /* uint8  [num_envs][84][84] gray observation */
+    NESLE_VIEW_COUNT = 13
+};
+
+/* nesle_render outputs (bit mask). */
+enum {
+    NESLE_FRAME_RGB = 1,
+    NESLE_FRAME_PALETTE = 2,
+    NESLE_FRAME_GRAY84 = 4
 };
 
 enum { NESLE_DTYPE_U8 = 0, NESLE_DTYPE_I64 = 1, NESLE_DTYPE_F32 = 2, NESLE_DTYPE_U32 = 3, NESLE_DTYPE_U64 = 4 };
@@ -71,12 +81,14 @@ typedef struct nesle_config {
     uint32_t x_lo, x_hi, done_addr, clip;
     float time_penalty;
     int32_t device;                      /* HIP device ordinal, -1 = current device    */
+    uint32_t frames;                     /* 1 (default): keep the presentation snapshot
+                                            that nesle_render draws; 0: RAM-only batch */
 } nesle_config;
 
 typedef struct nesle_view {
     void* data;         /* device pointer */
     int32_t ndim;
-    int64_t shape[2];
+    int64_t shape[4];
     int32_t dtype;      /* NESLE_DTYPE_* */
     int32_t device_id;
 } nesle_view;
@@ -92,7 +104,7 @@ typedef struct nesle_rom_info {
     uint32_t is_nes2;
 } nesle_rom_info;
 
-/* Defaults: SMB reward, frameskip 4, budget 200,000, current device. */
+/* Defaults: SMB reward, frameskip 4, budget 200,000, current device, frames on. */
 void nesle_config_init(nesle_config* cfg);
 
 /* Parse the iNES image, allocate device state, upload PRG/CHR and power every
@@ -135,13 +147,26 @@ int nesle_set_actions(nesle_batch* b, const void* actions, int dtype, int on_dev
 int nesle_step(nesle_batch* b, int auto_reset, int stats_mode);
 
 /* Device view of one buffer (NESLE_VIEW_*, not OAM).  Replaces
- * ram_device/rewards_device/last_done_device (cuda_module.cu:854-902). */
+ * ram_device/rewards_device/last_done_device (cuda_module.cu:854-902) and
+ * frames_device (cuda_module.cu:871-886).  A frame view exists once
+ * nesle_render has produced that output. */
 int nesle_get_view(nesle_batch* b, int kind, nesle_view* out);
 
 /* Synchronous copy of a view to host memory (bytes must equal its size).
  * Replaces ram()/oam() and the reward/done copies (cuda_module.cu:574-583,
  * 841-852, 904-915). */
 int nesle_copy_to_host(nesle_batch* b, int kind, void* dst, size_t bytes);
+
+/* Draw every console's frame from its presentation snapshot (frozen at the
+ * last vblank; seeded from live state by full resets and state loads) into
+ * the device buffers selected by `outputs` (NESLE_FRAME_*), allocated on
+ * first use.  RGB and palette values follow the batched renderer
+ * (batch_render.cuh:161-440, launched by render_device/launch_render_device,
+ * cuda_module.cu:1435-1438, 865-869); GRAY84 is the 84x84 luma observation
+ * of the reference's training wrappers (project/mario-rl-ram/src/mario_rl/
+ * wrappers.py:209-215, Pillow BILINEAR).  Fails with NESLE_EINVAL on a
+ * batch created with frames = 0.  Does not synchronise. */
+int nesle_render(nesle_batch* b, uint32_t outputs);
 
 /* Full state of one console as a canonical blob (host, NESLE_STATE_BYTES). */
 int nesle_save_state(nesle_batch* b, uint32_t env, uint8_t* out_blob);

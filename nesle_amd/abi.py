@@ -24,6 +24,8 @@ OK, EINVAL, ERUNTIME, EDEVICE = 0, 1, 2, 3
 REWARD_SMB, REWARD_XDELTA = 0, 1
 VIEW_RAM, VIEW_REWARDS, VIEW_DONES, VIEW_ACTIONS = 0, 1, 2, 3
 VIEW_INSTRUCTIONS, VIEW_FRAMES, VIEW_BUDGET_HITS, VIEW_OPCODES, VIEW_PCS, VIEW_OAM = 4, 5, 6, 7, 8, 9
+VIEW_FRAME_RGB, VIEW_FRAME_PALETTE, VIEW_GRAY84 = 10, 11, 12
+FRAME_RGB, FRAME_PALETTE, FRAME_GRAY84 = 1, 2, 4
 DTYPE_U8, DTYPE_I64, DTYPE_F32, DTYPE_U32, DTYPE_U64 = 0, 1, 2, 3, 4
 STATE_BYTES = 22896
 
@@ -42,6 +44,7 @@ class Config(ctypes.Structure):
         ("clip", ctypes.c_uint32),
         ("time_penalty", ctypes.c_float),
         ("device", ctypes.c_int32),
+        ("frames", ctypes.c_uint32),
     ]
 
 
@@ -49,7 +52,7 @@ class View(ctypes.Structure):
     _fields_ = [
         ("data", ctypes.c_void_p),
         ("ndim", ctypes.c_int32),
-        ("shape", ctypes.c_int64 * 2),
+        ("shape", ctypes.c_int64 * 4),
         ("dtype", ctypes.c_int32),
         ("device_id", ctypes.c_int32),
     ]
@@ -109,6 +112,7 @@ def lib():
         "nesle_step": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int]),
         "nesle_get_view": (ctypes.c_int, [vp, ctypes.c_int, ctypes.POINTER(View)]),
         "nesle_copy_to_host": (ctypes.c_int, [vp, ctypes.c_int, vp, ctypes.c_size_t]),
+        "nesle_render": (ctypes.c_int, [vp, ctypes.c_uint32]),
         "nesle_save_state": (ctypes.c_int, [vp, ctypes.c_uint32, _U8P]),
         "nesle_load_state": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.c_size_t, _U8P]),
         "nesle_snapshot_capture": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32]),
@@ -161,7 +165,8 @@ class Batch:
 
     def __init__(self, rom: bytes, num_envs: int, frameskip: int = 4, *, reward_kind: int = REWARD_SMB,
                  x_lo: int = 0x86, x_hi: int = 0x6D, done_addr: int = 0, clip: int = 15,
-                 time_penalty: float = 0.0, max_instructions_per_frame: int = 0, device: int = -1) -> None:
+                 time_penalty: float = 0.0, max_instructions_per_frame: int = 0, device: int = -1,
+                 frames: bool = True) -> None:
         L = lib()
         cfg = Config()
         L.nesle_config_init(ctypes.byref(cfg))
@@ -170,6 +175,7 @@ class Batch:
         cfg.reward_kind, cfg.x_lo, cfg.x_hi, cfg.done_addr, cfg.clip = reward_kind, x_lo, x_hi, done_addr, clip
         cfg.time_penalty = time_penalty
         cfg.device = device
+        cfg.frames = int(frames)
         h = ctypes.c_void_p()
         _check(L.nesle_create(ctypes.byref(cfg), rom, len(rom), ctypes.byref(h)))
         self.h = h
@@ -228,10 +234,16 @@ class Batch:
               VIEW_DONES: (np.uint8, (self.n,)), VIEW_ACTIONS: (np.uint8, (self.n,)),
               VIEW_INSTRUCTIONS: (np.uint64, (self.n,)), VIEW_FRAMES: (np.uint32, (self.n,)),
               VIEW_BUDGET_HITS: (np.uint32, (self.n,)), VIEW_OPCODES: (np.uint64, (256,)),
-              VIEW_PCS: (np.uint64, (65536,)), VIEW_OAM: (np.uint8, (self.n, 256))}[kind]
+              VIEW_PCS: (np.uint64, (65536,)), VIEW_OAM: (np.uint8, (self.n, 256)),
+              VIEW_FRAME_RGB: (np.uint8, (self.n, 240, 256, 3)), VIEW_FRAME_PALETTE: (np.uint8, (self.n, 240, 256)),
+              VIEW_GRAY84: (np.uint8, (self.n, 84, 84))}[kind]
         out = np.empty(dt[1], dtype=dt[0])
         _check(lib().nesle_copy_to_host(self.h, kind, out.ctypes.data, out.nbytes))
         return out
+
+    def render(self, outputs: int = FRAME_RGB) -> None:
+        """Draw every console's presentation snapshot into the FRAME_* outputs."""
+        _check(lib().nesle_render(self.h, outputs))
 
     def save_state(self, env: int) -> np.ndarray:
         out = np.empty(STATE_BYTES, dtype=np.uint8)

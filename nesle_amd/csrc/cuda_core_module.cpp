@@ -59,7 +59,7 @@ constexpr std::uint8_t kDLInt = 0, kDLUInt = 1, kDLFloat = 2;
 
 struct Managed {
     DLManagedTensor t{};
-    std::int64_t shape[2] = {0, 0};
+    std::int64_t shape[4] = {0, 0, 0, 0};
     nesle_batch* owner = nullptr;
 };
 
@@ -193,7 +193,7 @@ struct RewardSpec {
 class CudaBatch {
 public:
     CudaBatch(std::uint32_t num_envs, std::uint32_t frameskip, const py::bytes& rom, const RewardSpec& r,
-              std::int32_t device, std::uint32_t max_instructions) {
+              std::int32_t device, std::uint32_t max_instructions, bool frames) {
         nesle_config cfg;
         nesle_config_init(&cfg);
         cfg.num_envs = num_envs;
@@ -206,6 +206,8 @@ public:
         cfg.clip = r.clip;
         cfg.time_penalty = r.time_penalty;
         cfg.device = device;
+        cfg.frames = frames ? 1u : 0u;
+        frames_ = frames;
         const auto bytes = bytes_vec(rom);
         check(nesle_create(&cfg, bytes.data(), bytes.size(), &h_));
         n_ = num_envs;
@@ -248,12 +250,26 @@ public:
         check(nesle_set_actions(h_, v.ptr, NESLE_DTYPE_U8, 0));
     }
 
-    // reset(): power-on or snapshot reset of every console; returns the RAM
-    // observation (the RGB frame of the reference's reset() belongs to the
-    // renderer).
+    // reset(): power-on or snapshot reset of every console, then the RGB
+    // frames of the re-seeded presentation snapshot (cuda_module.cu:469-479);
+    // a batch without frames returns the RAM observation instead.
     py::array_t<std::uint8_t> reset() {
         check(nesle_reset(h_));
-        return ram();
+        return frames_ ? render() : ram();
+    }
+
+    // Host RGB frames [N, 240, 256, 3], re-rendered first
+    // (cuda_module.cu:820-839).
+    py::array_t<std::uint8_t> render() {
+        check(nesle_render(h_, NESLE_FRAME_RGB));
+        return host<std::uint8_t>(NESLE_VIEW_FRAME_RGB, {py::ssize_t(n_), 240, 256, 3});
+    }
+
+    // One render launch producing any of the device outputs.
+    void render_frames_device(bool rgb, bool palette, bool gray84) {
+        const std::uint32_t outputs = (rgb ? NESLE_FRAME_RGB : 0u) | (palette ? NESLE_FRAME_PALETTE : 0u) |
+                                      (gray84 ? NESLE_FRAME_GRAY84 : 0u);
+        check(nesle_render(h_, outputs));
     }
 
     DeviceArrayView reset_device() {
@@ -261,14 +277,20 @@ public:
         return view(NESLE_VIEW_RAM);
     }
 
+    // step(actions, render_frame, copy_obs) (cuda_module.cu:533-592): one
+    // env-step, a render when either flag is set, and the RGB frames as
+    // "obs" when copy_obs (the RAM observation on a batch without frames).
     py::dict step(const py::array_t<std::uint8_t, py::array::c_style | py::array::forcecast>& actions,
-                  bool /*render_frame*/, bool copy_obs) {
+                  bool render_frame, bool copy_obs) {
         set_host_actions(actions);
         check(nesle_step(h_, 0, 0));
+        if (frames_ && (render_frame || copy_obs)) check(nesle_render(h_, NESLE_FRAME_RGB));
         py::dict out;
+        if (copy_obs) {
+            out["obs"] = frames_ ? host<std::uint8_t>(NESLE_VIEW_FRAME_RGB, {py::ssize_t(n_), 240, 256, 3}) : ram();
+        }
         out["rewards"] = host<float>(NESLE_VIEW_REWARDS, {py::ssize_t(n_)});
         out["dones"] = host<std::uint8_t>(NESLE_VIEW_DONES, {py::ssize_t(n_)});
-        if (copy_obs) out["obs"] = ram();
         return out;
     }
 
@@ -363,12 +385,14 @@ public:
     std::uint32_t frameskip() const { return nesle_frameskip(h_); }
     std::uint32_t num_levels() const { return nesle_num_levels(h_); }
     bool has_snapshot() const { return has_snapshot_ && nesle_num_levels(h_) > 0; }
+    bool frames() const { return frames_; }
     int device_id() const { return nesle_device_id(h_); }
 
 private:
     nesle_batch* h_ = nullptr;
     std::uint32_t n_ = 0;
     bool has_snapshot_ = false;
+    bool frames_ = true;
 };
 
 RewardSpec reward_from_kwargs(const py::kwargs& kw) {
@@ -399,6 +423,8 @@ std::int32_t device_from_kwargs(const py::kwargs& kw) {
 std::uint32_t budget_from_kwargs(const py::kwargs& kw) {
     return kw.contains("max_instructions_per_frame") ? kw["max_instructions_per_frame"].cast<std::uint32_t>() : 0u;
 }
+
+bool frames_from_kwargs(const py::kwargs& kw) { return kw.contains("frames") ? kw["frames"].cast<bool>() : true; }
 
 }  // namespace
 
@@ -467,13 +493,13 @@ PYBIND11_MODULE(_cuda_core_native, m) {
              py::arg("num_envs"), py::arg("frameskip"))
         .def(py::init([](std::uint32_t num_envs, std::uint32_t frameskip, const py::bytes& rom, const py::kwargs& kw) {
                  return new CudaBatch(num_envs, frameskip, rom, reward_from_kwargs(kw), device_from_kwargs(kw),
-                                      budget_from_kwargs(kw));
+                                      budget_from_kwargs(kw), frames_from_kwargs(kw));
              }),
              py::arg("num_envs"), py::arg("frameskip"), py::arg("rom_bytes"))
         .def(py::init([](std::uint32_t num_envs, std::uint32_t frameskip, const py::bytes& rom, const py::bytes& snap,
                          const py::kwargs& kw) {
                  auto* b = new CudaBatch(num_envs, frameskip, rom, reward_from_kwargs(kw), device_from_kwargs(kw),
-                                         budget_from_kwargs(kw));
+                                         budget_from_kwargs(kw), frames_from_kwargs(kw));
                  try {
                      b->set_snapshots({snap}, nullptr);
                  } catch (...) {
@@ -493,7 +519,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
                      throw py::value_error("env_to_level must have shape (num_envs,)");
                  std::vector<std::uint8_t> levels(env_to_level.data(), env_to_level.data() + num_envs);
                  auto* b = new CudaBatch(num_envs, frameskip, rom, reward_from_kwargs(kw), device_from_kwargs(kw),
-                                         budget_from_kwargs(kw));
+                                         budget_from_kwargs(kw), frames_from_kwargs(kw));
                  try {
                      b->set_snapshots(snaps, &levels);
                  } catch (...) {
@@ -515,6 +541,13 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("step_profile", [](CudaBatch& b, const py::array_t<std::uint8_t, py::array::c_style | py::array::forcecast>& a) {
                  return b.step_stats(a, 2);
              }, py::arg("actions"))
+        .def("render", &CudaBatch::render)
+        .def("render_device", [](CudaBatch& b) { b.render_frames_device(true, false, false); })
+        .def("render_frames_device", &CudaBatch::render_frames_device, py::arg("rgb") = true,
+             py::arg("palette") = false, py::arg("gray84") = false)
+        .def("frames_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_FRAME_RGB); })
+        .def("palette_frames_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_FRAME_PALETTE); })
+        .def("gray84_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_GRAY84); })
         .def("ram", &CudaBatch::ram)
         .def("oam", &CudaBatch::oam)
         .def("ram_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_RAM); })
@@ -534,6 +567,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("set_stream", &CudaBatch::set_stream, py::arg("stream"))
         .def_property_readonly("name", [](const CudaBatch&) { return std::string("cuda-console"); })
         .def_property_readonly("has_snapshot", &CudaBatch::has_snapshot)
+        .def_property_readonly("frames", &CudaBatch::frames)
         .def_property_readonly("num_levels", &CudaBatch::num_levels)
         .def_property_readonly("num_envs", &CudaBatch::num_envs)
         .def_property_readonly("frameskip", &CudaBatch::frameskip)

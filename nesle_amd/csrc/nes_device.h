@@ -85,6 +85,20 @@ __device__ __forceinline__ std::uint64_t le64(const std::uint8_t* b, std::uint32
     return le32(b, o) | (static_cast<std::uint64_t>(le32(b, o + 4)) << 32);
 }
 
+// Console `env`'s video memory block (palette, OAM, nametables; vram::*).
+__device__ __forceinline__ std::uint8_t* vram_of(const DeviceState& s, std::uint32_t env) {
+    return s.vram + static_cast<std::size_t>(env) * s.vram_stride;
+}
+
+// 16-byte copies and fills; every video memory section and blob field they
+// are used on starts on a 16-byte boundary and is a multiple of 16 long.
+__device__ __forceinline__ void copy16(std::uint8_t* dst, const std::uint8_t* src, std::uint32_t bytes) {
+    for (std::uint32_t i = 0; i < bytes / 16; ++i) reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+}
+__device__ __forceinline__ void zero16(std::uint8_t* dst, std::uint32_t bytes) {
+    for (std::uint32_t i = 0; i < bytes / 16; ++i) reinterpret_cast<uint4*>(dst)[i] = make_uint4(0, 0, 0, 0);
+}
+
 // Load a canonical blob into console `env` (all fields, arrays included).
 __device__ inline void load_blob(const DeviceState& s, std::uint32_t env, const std::uint8_t* b) {
     using namespace blob;
@@ -104,9 +118,10 @@ __device__ inline void load_blob(const DeviceState& s, std::uint32_t env, const 
     for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * pitch + env] = b[kApuIo + i];
     for (std::uint32_t i = 0; i < kRamBytes; ++i) s.ram[i * pitch + env] = b[kRam + i];
     for (std::uint32_t i = 0; i < kPrgRamBytes; ++i) s.prg_ram[i * pitch + env] = b[kPrgRam + i];
-    for (std::uint32_t i = 0; i < kOamBytes; ++i) s.oam[i * pitch + env] = b[kOam + i];
-    for (std::uint32_t i = 0; i < kPaletteBytes; ++i) s.palette[i * pitch + env] = b[kPalette + i];
-    for (std::uint32_t i = 0; i < s.nt_bytes; ++i) s.nametable[i * pitch + env] = b[kNametable + i];
+    std::uint8_t* vm = vram_of(s, env);
+    copy16(vm + vram::kOam, b + kOam, kOamBytes);
+    copy16(vm + vram::kPalette, b + kPalette, kPaletteBytes);
+    copy16(vm + vram::kNametable, b + kNametable, s.nt_bytes);
     if (s.chr_ram != nullptr)
         for (std::uint32_t i = 0; i < kChrRamBytes; ++i) s.chr_ram[i * pitch + env] = b[kChrRam + i];
 }
@@ -127,9 +142,7 @@ __device__ inline void cold_reset(const DeviceState& s, std::uint32_t env, const
     for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * pitch + env] = 0;
     for (std::uint32_t i = 0; i < kRamBytes; ++i) s.ram[i * pitch + env] = 0;
     for (std::uint32_t i = 0; i < kPrgRamBytes; ++i) s.prg_ram[i * pitch + env] = 0;
-    for (std::uint32_t i = 0; i < kOamBytes; ++i) s.oam[i * pitch + env] = 0;
-    for (std::uint32_t i = 0; i < kPaletteBytes; ++i) s.palette[i * pitch + env] = 0;
-    for (std::uint32_t i = 0; i < s.nt_bytes; ++i) s.nametable[i * pitch + env] = 0;
+    zero16(vram_of(s, env), s.vram_stride);
     if (s.chr_ram != nullptr)
         for (std::uint32_t i = 0; i < kChrRamBytes; ++i) s.chr_ram[i * pitch + env] = 0;
 }

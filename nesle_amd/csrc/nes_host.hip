@@ -18,6 +18,7 @@
 #include "../../include/nesle_hip.h"
 #include "nes_launch.h"
 #include "nes_layout.h"
+#include "nes_render.h"
 
 using nesle::DeviceState;
 namespace blob = nesle::blob;
@@ -221,6 +222,11 @@ struct nesle_batch {
     std::uint32_t num_levels = 0;
     std::uint32_t bank_capacity = 0;
     void* stats_arena = nullptr;
+    // Frames: render outputs (allocated on first use) and the resample tables.
+    std::uint8_t* d_frame_rgb = nullptr;
+    std::uint8_t* d_frame_palette = nullptr;
+    std::uint8_t* d_gray84 = nullptr;
+    void* d_render_tables = nullptr;   // render::Taps, then the 64-entry gray LUT
     // Step-kernel timing: event pairs are recorded per launch and folded into
     // the totals once the pair has completed.
     bool timing = false;
@@ -236,6 +242,10 @@ struct nesle_batch {
         (void)hipFree(arena);
         (void)hipFree(d_bank);
         (void)hipFree(stats_arena);
+        (void)hipFree(d_frame_rgb);
+        (void)hipFree(d_frame_palette);
+        (void)hipFree(d_gray84);
+        (void)hipFree(d_render_tables);
     }
 
     void activate() const { hip_check(hipSetDevice(device), "hipSetDevice"); }
@@ -263,10 +273,12 @@ struct nesle_batch {
         // so the step kernel reaches both with one row * pitch + env offset.
         // Plus one spare row that the step kernel's lanes with nothing to store write to.
         add(&ds.ram, static_cast<std::size_t>(nesle::kRamBytes + nesle::kPrgRamBytes + 1) * P);
-        add(&ds.oam, nesle::kOamBytes * P);
-        add(&ds.palette, nesle::kPaletteBytes * P);
-        add(&ds.nametable, static_cast<std::size_t>(ds.nt_bytes) * P);
+        add(&ds.vram, static_cast<std::size_t>(ds.vram_stride) * n);
         if (rom.chr.empty()) add(&ds.chr_ram, nesle::kChrRamBytes * P);
+        if (cfg.frames) {
+            add(&ds.present, static_cast<std::size_t>(nesle::present::kHeader + ds.vram_stride) * n);
+            add(&ds.lat_sx, n); add(&ds.lat_sy, n); add(&ds.lat_ctrl, n);
+        }
         std::uint8_t* actions = nullptr;
         add(&actions, n);
         add(&ds.rewards, 4 * n); add(&ds.done, n); add(&ds.prev_x, 4 * n); add(&ds.prev_time, 4 * n);
@@ -304,6 +316,32 @@ struct nesle_batch {
     }
 
     void refresh_obs() { hip_check(nesle::launch_ram_obs(ds, d_obs, stream), "ram_obs_kernel"); }
+
+    // Presentation snapshot from live state (full resets, state loads).
+    void seed_present(const std::uint8_t* dmask) {
+        hip_check(nesle::launch_seed_present(ds, dmask, stream), "seed_present_kernel");
+    }
+
+    std::uint8_t* frame_buffer(int output) {
+        const std::size_t n = cfg.num_envs;
+        std::uint8_t** slot = output == NESLE_FRAME_RGB ? &d_frame_rgb
+                              : output == NESLE_FRAME_PALETTE ? &d_frame_palette : &d_gray84;
+        const std::size_t bytes = output == NESLE_FRAME_RGB ? n * 240 * 256 * 3
+                                  : output == NESLE_FRAME_PALETTE ? n * 240 * 256
+                                                                  : n * nesle::render::kOut * nesle::render::kOut;
+        if (*slot == nullptr) hip_check(hipMalloc(slot, bytes), "hipMalloc frame buffer");
+        return *slot;
+    }
+
+    void ensure_render_tables() {
+        if (d_render_tables != nullptr) return;
+        const nesle::render::Taps taps = nesle::render::make_taps();
+        std::vector<std::uint8_t> host(sizeof(taps) + 64);
+        std::memcpy(host.data(), &taps, sizeof(taps));
+        nesle::render::make_gray_lut(host.data() + sizeof(taps));
+        hip_check(hipMalloc(&d_render_tables, host.size()), "hipMalloc render tables");
+        host_to_device(d_render_tables, host.data(), host.size(), "upload render tables");
+    }
 
     std::pair<hipEvent_t, hipEvent_t> take_events() {
         if (!spare.empty()) {
@@ -372,6 +410,7 @@ void nesle_config_init(nesle_config* cfg) {
     cfg->done_addr = 0;
     cfg->clip = 15;
     cfg->device = -1;
+    cfg->frames = 1;
 }
 
 int nesle_parse_ines(const std::uint8_t* bytes, std::size_t len, nesle_rom_info* out) {
@@ -411,6 +450,7 @@ int nesle_create(const nesle_config* cfg, const std::uint8_t* ines, std::size_t 
         s.pitch = b->pitch;
         s.nt_mode = b->rom.info.nametable_arrangement;
         s.nt_bytes = s.nt_mode == 2 ? 4096u : 2048u;
+        s.vram_stride = nesle::vram::stride(s.nt_bytes);
         s.prg_mask = static_cast<std::uint32_t>(b->rom.prg.size() - 1);
         s.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
         s.reward_kind = b->cfg.reward_kind;
@@ -423,6 +463,7 @@ int nesle_create(const nesle_config* cfg, const std::uint8_t* ines, std::size_t 
         b->host_to_device(b->d_prg, b->rom.prg.data(), b->rom.prg.size(), "upload PRG ROM");
         if (!b->rom.chr.empty()) b->host_to_device(b->d_chr, b->rom.chr.data(), b->rom.chr.size(), "upload CHR ROM");
         hip_check(nesle::launch_reset(s, nullptr, b->stream), "reset_kernel");
+        b->seed_present(nullptr);
         b->refresh_obs();
         b->sync();
         *out = b.release();
@@ -460,6 +501,7 @@ int nesle_set_snapshots(nesle_batch* b, const std::uint8_t* const* blobs, const 
         b->ds.env_to_level = b->d_levels;
         b->ds.num_levels = count;
         hip_check(nesle::launch_reset(b->ds, nullptr, b->stream), "reset_kernel");
+        b->seed_present(nullptr);
         b->refresh_obs();
         b->sync();
     });
@@ -478,6 +520,7 @@ int nesle_reset(nesle_batch* b) {
         if (b == nullptr) throw InvalidArgument("null batch");
         b->activate();
         hip_check(nesle::launch_reset(b->ds, nullptr, b->stream), "reset_kernel");
+        b->seed_present(nullptr);
         b->refresh_obs();
         b->sync();
     });
@@ -572,6 +615,10 @@ int nesle_get_view(nesle_batch* b, int kind, nesle_view* out) {
         v.device_id = b->device;
         v.ndim = 1;
         v.shape[0] = n;
+        auto frame = [&](std::uint8_t* buf, std::int32_t ndim, std::int64_t h, std::int64_t w, std::int64_t c) {
+            if (buf == nullptr) throw InvalidArgument("no frames yet: call nesle_render with this output first");
+            v.data = buf; v.ndim = ndim; v.shape[1] = h; v.shape[2] = w; v.shape[3] = c; v.dtype = NESLE_DTYPE_U8;
+        };
         switch (kind) {
             case NESLE_VIEW_RAM: v.data = b->d_obs; v.ndim = 2; v.shape[1] = nesle::kRamBytes; v.dtype = NESLE_DTYPE_U8; break;
             case NESLE_VIEW_REWARDS: v.data = b->ds.rewards; v.dtype = NESLE_DTYPE_F32; break;
@@ -582,6 +629,9 @@ int nesle_get_view(nesle_batch* b, int kind, nesle_view* out) {
             case NESLE_VIEW_BUDGET_HITS: b->ensure_stats(); v.data = b->ds.stat_budget_hits; v.dtype = NESLE_DTYPE_U32; break;
             case NESLE_VIEW_OPCODES: b->ensure_stats(); v.data = b->ds.prof_opcodes; v.shape[0] = 256; v.dtype = NESLE_DTYPE_U64; break;
             case NESLE_VIEW_PCS: b->ensure_stats(); v.data = b->ds.prof_pcs; v.shape[0] = 65536; v.dtype = NESLE_DTYPE_U64; break;
+            case NESLE_VIEW_FRAME_RGB: frame(b->d_frame_rgb, 4, 240, 256, 3); break;
+            case NESLE_VIEW_FRAME_PALETTE: frame(b->d_frame_palette, 3, 240, 256, 0); break;
+            case NESLE_VIEW_GRAY84: frame(b->d_gray84, 3, nesle::render::kOut, nesle::render::kOut, 0); break;
             default: throw InvalidArgument("unknown view kind");
         }
         *out = v;
@@ -595,22 +645,44 @@ int nesle_copy_to_host(nesle_batch* b, int kind, void* dst, std::size_t bytes) {
         if (kind == NESLE_VIEW_OAM) {
             const std::size_t n = b->n();
             if (bytes != n * nesle::kOamBytes) throw InvalidArgument("OAM copy needs num_envs * 256 bytes");
-            std::vector<std::uint8_t> inter(static_cast<std::size_t>(nesle::kOamBytes) * b->pitch);
-            hip_check(hipMemcpyAsync(inter.data(), b->ds.oam, inter.size(), hipMemcpyDeviceToHost, b->stream), "copy oam");
+            hip_check(hipMemcpy2DAsync(dst, nesle::kOamBytes, b->ds.vram + nesle::vram::kOam, b->ds.vram_stride,
+                                       nesle::kOamBytes, n, hipMemcpyDeviceToHost, b->stream),
+                      "copy oam");
             b->sync();
-            auto* o = static_cast<std::uint8_t*>(dst);
-            for (std::size_t e = 0; e < n; ++e)
-                for (std::size_t i = 0; i < nesle::kOamBytes; ++i) o[e * nesle::kOamBytes + i] = inter[i * b->pitch + e];
             return;
         }
         nesle_view v{};
         if (nesle_get_view(b, kind, &v) != NESLE_OK) throw InvalidArgument(g_error);
         static const std::size_t kSize[] = {1, 8, 4, 4, 8};
-        std::size_t want = kSize[v.dtype] * static_cast<std::size_t>(v.shape[0]) * (v.ndim == 2 ? v.shape[1] : 1);
+        std::size_t want = kSize[v.dtype];
+        for (int d = 0; d < v.ndim; ++d) want *= static_cast<std::size_t>(v.shape[d]);
         if (bytes != want) throw InvalidArgument("host buffer has " + std::to_string(bytes) + " bytes, view needs " +
                                                  std::to_string(want));
         hip_check(hipMemcpyAsync(dst, v.data, bytes, hipMemcpyDeviceToHost, b->stream), "copy view to host");
         b->sync();
+    });
+}
+
+int nesle_render(nesle_batch* b, std::uint32_t outputs) {
+    return guarded([&] {
+        if (b == nullptr) throw InvalidArgument("null batch");
+        if (outputs == 0 || (outputs & ~7u) != 0) throw InvalidArgument("outputs must be a non-empty set of NESLE_FRAME_* bits");
+        if (b->ds.present == nullptr) throw InvalidArgument("frames are off for this batch (created with frames = 0)");
+        b->activate();
+        b->ensure_render_tables();
+        nesle::RenderArgs a{};
+        a.n = b->n();
+        a.present = b->ds.present;
+        a.present_stride = nesle::present::kHeader + b->ds.vram_stride;
+        a.chr = b->rom.chr.empty() ? nullptr : b->d_chr;
+        a.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
+        a.nt_mode = b->ds.nt_mode;
+        a.taps = static_cast<const nesle::render::Taps*>(b->d_render_tables);
+        a.gray_lut = static_cast<const std::uint8_t*>(b->d_render_tables) + sizeof(nesle::render::Taps);
+        a.rgb = (outputs & NESLE_FRAME_RGB) ? b->frame_buffer(NESLE_FRAME_RGB) : nullptr;
+        a.palette = (outputs & NESLE_FRAME_PALETTE) ? b->frame_buffer(NESLE_FRAME_PALETTE) : nullptr;
+        a.gray = (outputs & NESLE_FRAME_GRAY84) ? b->frame_buffer(NESLE_FRAME_GRAY84) : nullptr;
+        hip_check(nesle::launch_render(a, b->stream), "render_kernel");
     });
 }
 
@@ -637,6 +709,7 @@ int nesle_load_state(nesle_batch* b, const std::uint8_t* data, std::size_t len, 
             dmask = b->d_mask;
         }
         hip_check(nesle::launch_load_blob(b->ds, b->d_blob, dmask, b->stream), "load_blob_kernel");
+        b->seed_present(dmask);
         b->refresh_obs();
         b->sync();
     });

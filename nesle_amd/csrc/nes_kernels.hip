@@ -76,12 +76,12 @@ __global__ void __launch_bounds__(kBlock) save_blob_kernel(DeviceState s, std::u
     } else if (i < kOam) {
         v = s.prg_ram[(i - kPrgRam) * pitch + env];
     } else if (i < kPalette) {
-        v = s.oam[(i - kOam) * pitch + env];
+        v = vram_of(s, env)[vram::kOam + i - kOam];
     } else if (i < kNametable) {
-        v = s.palette[(i - kPalette) * pitch + env];
+        v = vram_of(s, env)[vram::kPalette + i - kPalette];
     } else if (i < kChrRam) {
         const std::uint32_t k = i - kNametable;
-        v = k < s.nt_bytes ? s.nametable[k * pitch + env] : 0;
+        v = k < s.nt_bytes ? vram_of(s, env)[vram::kNametable + k] : 0;
     } else {
         v = s.chr_ram != nullptr ? s.chr_ram[(i - kChrRam) * pitch + env] : 0;
     }
@@ -122,6 +122,31 @@ __global__ void __launch_bounds__(kBlock) seed_kernel(DeviceState s) {
     if (env < s.n) seed_baselines(s, env);
 }
 
+// Presentation snapshot from live state, so a render right after a reset or
+// state load is coherent (cuda_module.cu:1440-1463): one workgroup per
+// console (selected by mask, null = all) copies its video memory block.
+__global__ void __launch_bounds__(kBlock) seed_present_kernel(DeviceState s, const std::uint8_t* mask) {
+    const std::uint32_t env = blockIdx.x;
+    if (mask != nullptr && mask[env] == 0) return;
+    const std::uint32_t vs = s.vram_stride;
+    std::uint8_t* rec = s.present + static_cast<std::size_t>(env) * (present::kHeader + vs);
+    const std::uint32_t t = threadIdx.x;
+    if (t < present::kHeader) {
+        const std::uint32_t sx = s.scroll_x[env], sy = s.scroll_y[env], ctrl = s.ctrl[env];
+        const std::uint32_t k = t % 3;
+        const std::uint32_t v = t == present::kMask ? s.mask[env] : t > present::kMask ? 0u : (k == 0 ? sx : k == 1 ? sy : ctrl);
+        rec[t] = static_cast<std::uint8_t>(v);
+        if (t == 0) {
+            s.lat_sx[env] = static_cast<std::uint8_t>(sx);
+            s.lat_sy[env] = static_cast<std::uint8_t>(sy);
+            s.lat_ctrl[env] = static_cast<std::uint8_t>(ctrl);
+        }
+    }
+    const auto* from = reinterpret_cast<const std::uint32_t*>(vram_of(s, env));
+    auto* to = reinterpret_cast<std::uint32_t*>(rec + present::kHeader);
+    for (std::uint32_t i = t; i < vs / 4; i += kBlock) to[i] = from[i];
+}
+
 inline std::uint32_t blocks_for(std::uint32_t n) { return (n + kBlock - 1) / kBlock; }
 
 }  // namespace
@@ -155,6 +180,12 @@ hipError_t launch_actions_i64(std::uint8_t* dst, const long long* src, std::uint
 
 hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32_t value, hipStream_t stream) {
     poke_ram_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, addr, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream) {
+    if (s.n == 0 || s.present == nullptr) return hipSuccess;
+    seed_present_kernel<<<dim3(s.n), dim3(kBlock), 0, stream>>>(s, mask);
     return hipGetLastError();
 }
 

@@ -21,5 +21,7 @@ hipError_t launch_ram_obs(const DeviceState& s, std::uint8_t* obs, hipStream_t s
 hipError_t launch_actions_i64(std::uint8_t* dst, const long long* src, std::uint32_t n, hipStream_t stream);
 hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32_t value, hipStream_t stream);
 hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
+// Presentation snapshot (and pre-render latch) from live state, masked.
+hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
 
 }  // namespace nesle

@@ -1,15 +1,21 @@
 // nes_layout.h -- device state layout shared by the HIP kernels
 // (nes_step.hip, nes_kernels.hip) and the host library (nes_host.hip).
 //
-// HBM layout.  Every per-console byte array is interleaved "address-major":
-// element (addr, env) lives at base[addr * pitch + env], with pitch = num_envs
-// rounded up to 256.  Lanes of a wave64 are consecutive envs, so when they
-// touch the same NES address (same code path, same zero-page variable) the
-// wave issues one 64-byte access instead of 64 scattered ones, and a 128-byte
-// cache line holds one NES address for 128 consecutive consoles.  Per-env
-// scalars are plain SoA arrays indexed by env.  The env-major RAM observation
-// that callers see ([num_envs][2048], the reference's layout at
-// cpp/bindings/cuda_module.cu:854-863) is produced by a transpose kernel.
+// HBM layout.  CPU-side byte arrays (RAM, PRG RAM, APU/IO registers, CHR RAM)
+// are interleaved "address-major": element (addr, env) lives at
+// base[addr * pitch + env], with pitch = num_envs rounded up to 256.  Lanes of
+// a wave64 are consecutive envs, so when they touch the same NES address (same
+// code path, same zero-page variable) the wave issues one 64-byte access
+// instead of 64 scattered ones, and a 128-byte cache line holds one NES
+// address for 128 consecutive consoles.  Per-env scalars are plain SoA arrays
+// indexed by env.  The env-major RAM observation that callers see
+// ([num_envs][2048], the reference's layout at cpp/bindings/cuda_module.cu:
+// 854-863) is produced by a transpose kernel.
+//
+// Video memory (palette, OAM, nametables) is env-major instead: one block of
+// vram_stride bytes per console (vram::*).  Only the I/O paths touch it, one
+// console at a time, and the vblank presentation snapshot copies a whole
+// block, which is then one contiguous run per console.
 #pragma once
 
 #include <cstdint>
@@ -97,10 +103,10 @@ struct DeviceState {
     std::uint8_t* apu_io;
     std::uint8_t* ram;
     std::uint8_t* prg_ram;     // = ram + 2048 * pitch (RAM and PRG RAM are one array)
-    std::uint8_t* oam;
-    std::uint8_t* palette;
-    std::uint8_t* nametable;
     std::uint8_t* chr_ram;     // null when the cart has CHR ROM
+    // Env-major video memory: [n][vram_stride] (vram::* offsets).
+    std::uint8_t* vram;
+    std::uint32_t vram_stride;
 
     // Step inputs/outputs.
     const std::uint8_t* actions;   // [n] controller masks for this step
@@ -123,6 +129,34 @@ struct DeviceState {
     const std::uint8_t* bank;
     const std::uint8_t* env_to_level;
     std::uint32_t num_levels;
+
+    // Presentation snapshot (null when frames are off): one record of
+    // present::kHeader + vram_stride bytes per console, frozen at a vblank,
+    // and the scroll/ctrl latched at the pre-render line (batch_ppu.cuh:
+    // 215-260).
+    std::uint8_t* present;     // [n][present::kHeader + vram_stride]
+    std::uint8_t* lat_sx;      // [n]
+    std::uint8_t* lat_sy;      // [n]
+    std::uint8_t* lat_ctrl;    // [n]
 };
+
+// Video memory block of one console: palette, OAM, then 2 KB of nametable
+// RAM (4 KB on four-screen carts).  vram_stride = kNametable + nt_bytes.
+namespace vram {
+constexpr std::uint32_t kPalette = 0, kOam = 32, kNametable = 288;
+constexpr std::uint32_t stride(std::uint32_t nt_bytes) { return kNametable + nt_bytes; }
+}  // namespace vram
+
+// Presentation record: scroll/ctrl at frame start (latched at the previous
+// pre-render line) and end (at vblank), the mask, then the console's video
+// memory block as it was at vblank.
+namespace present {
+constexpr std::uint32_t kSxStart = 0, kSyStart = 1, kCtrlStart = 2, kSxEnd = 3, kSyEnd = 4, kCtrlEnd = 5, kMask = 6;
+constexpr std::uint32_t kHeader = 16;
+constexpr std::uint32_t kPalette = kHeader + vram::kPalette, kOam = kHeader + vram::kOam;
+constexpr std::uint32_t kNametable = kHeader + vram::kNametable;
+constexpr std::uint32_t bytes(std::uint32_t nt_bytes) { return kHeader + vram::stride(nt_bytes); }
+constexpr std::uint32_t kMaxBytes = kHeader + vram::kNametable + 4096;   // 4,400
+}  // namespace present
 
 }  // namespace nesle

@@ -1,0 +1,49 @@
+// nes_render.h -- frame rendering of the batched console (nes_render.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace nesle {
+namespace render {
+
+constexpr int kPrecision = 22;             // Pillow's 8-bit resample fixed point
+constexpr std::uint32_t kOut = 84;         // gray observation is kOut x kOut
+constexpr std::uint32_t kHTaps = 9;        // 256 -> 84: ceil(256 / 84) * 2 + 1
+constexpr std::uint32_t kVTaps = 7;        // 240 -> 84: ceil(240 / 84) * 2 + 1
+
+// Per output column (h_) and row (v_): first input, input count, weights.
+struct Taps {
+    std::int32_t h_lo[kOut], h_n[kOut], h_k[kOut][kHTaps];
+    std::int32_t v_lo[kOut], v_n[kOut], v_k[kOut][kVTaps];
+};
+
+// Host: the resize weights of Pillow's BILINEAR filter for 256x240 -> 84x84
+// (libImaging/Resample.c precompute_coeffs + normalize_coeffs_8bpc).
+Taps make_taps();
+// Host: gray value of each of the 64 palette colours, uint8(fma(b, .114,
+// fma(g, .587, r * .299))) -- numpy's float luma of the RGB frame, truncated.
+void make_gray_lut(std::uint8_t* lut);
+// Host: the renderer's RGB palette (64 x 3).
+const std::uint8_t* nes_rgb();
+
+}  // namespace render
+
+struct RenderArgs {
+    std::uint32_t n;                 // consoles
+    const std::uint8_t* present;     // [n][present_stride] presentation records
+    std::uint32_t present_stride;    // present::kHeader + video memory block
+    const std::uint8_t* chr;         // CHR ROM (device), null for CHR RAM
+    std::uint32_t chr_size;          // 0 for CHR RAM
+    std::uint32_t nt_mode;           // 0 vertical, 1 horizontal, 2 four-screen
+    const std::uint8_t* gray_lut;    // [64] (device)
+    const render::Taps* taps;        // (device)
+    std::uint8_t* palette;           // [n][240][256] or null
+    std::uint8_t* rgb;               // [n][240][256][3] or null
+    std::uint8_t* gray;              // [n][84][84] or null
+};
+
+hipError_t launch_render(const RenderArgs& a, hipStream_t stream);
+
+}  // namespace nesle

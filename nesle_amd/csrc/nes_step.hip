@@ -77,7 +77,7 @@ constexpr std::uint32_t kBytes = 40;
 }  // namespace reg
 
 // Bits of a console's `flags` VGPR.
-constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4;
+constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4, kPresentPending = 8;
 
 // Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
 // write to (one spare byte per console after PRG RAM).
@@ -183,6 +183,10 @@ struct Console {
     }
     // Offset of (row, this console) in an address-major interleaved array.
     __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return __umul24(row, pitch) + env; }
+    // This console's video memory block (env-major).
+    __device__ __forceinline__ std::uint8_t* vmem() const {
+        return s.vram + static_cast<std::size_t>(env) * s.vram_stride;
+    }
     __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t ra) const {
         if (ram_in_lds(ra)) return lds[base + ram_lds_off(ra)];
         return s.ram[goff(ra)];
@@ -214,9 +218,9 @@ struct Console {
         }
         if (addr < 0x3F00) {
             if (addr >= 0x3000) addr -= 0x1000;
-            return s.nametable[goff(nt_index(addr))];
+            return vmem()[vram::kNametable + nt_index(addr)];
         }
-        return s.palette[goff(pal_index(addr))];
+        return vmem()[vram::kPalette + pal_index(addr)];
     }
     __device__ void vram_wr(std::uint32_t addr, std::uint32_t val) const {
         addr &= 0x3FFF;
@@ -226,10 +230,10 @@ struct Console {
         }
         if (addr < 0x3F00) {
             if (addr >= 0x3000) addr -= 0x1000;
-            s.nametable[goff(nt_index(addr))] = static_cast<std::uint8_t>(val);
+            vmem()[vram::kNametable + nt_index(addr)] = static_cast<std::uint8_t>(val);
             return;
         }
-        s.palette[goff(pal_index(addr))] = static_cast<std::uint8_t>(val);
+        vmem()[vram::kPalette + pal_index(addr)] = static_cast<std::uint8_t>(val);
     }
 
     // ---- I/O space $2000-$5FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
@@ -246,7 +250,7 @@ struct Console {
                 w8(reg::kOpenBus, val);
                 return val;
             }
-            if (reg == 4) return s.oam[goff(r8(reg::kOamAddr))];
+            if (reg == 4) return vmem()[vram::kOam + r8(reg::kOamAddr)];
             if (reg == 7) {
                 const std::uint32_t v = r16(reg::kV);
                 const std::uint32_t va = v & 0x3FFF;
@@ -302,7 +306,7 @@ struct Console {
             w8(reg::kOamAddr, val);
         } else if (r == 4) {
             const std::uint32_t oa = r8(reg::kOamAddr);
-            s.oam[goff(oa)] = static_cast<std::uint8_t>(val);
+            vmem()[vram::kOam + oa] = static_cast<std::uint8_t>(val);
             w8(reg::kOamAddr, oa + 1);
         } else if (r == 5) {
             const std::uint32_t t = r16(reg::kT);
@@ -369,8 +373,12 @@ struct Console {
 
     // ---- PPU timing (ppu.hpp:46-76) -------------------------------------------------
     // Advance by `dots` (less than one frame past the next frame end), applying
-    // every event crossed in order.  Returns frames completed (0 or 1).
-    __device__ std::uint32_t settle(std::uint32_t dots) {
+    // every event crossed in order.  Returns frames completed (0 or 1).  Only
+    // the last vblank of the step reaches the presentation snapshot that a
+    // render after the step sees, so earlier ones are not captured unless
+    // `every_vblank` (frames cut short by the instruction budget, a console
+    // that stopped).
+    __device__ std::uint32_t settle(std::uint32_t dots, bool every_vblank) {
         const std::uint32_t start = r32(reg::kFrameDot), end = start + dots;
         const std::uint32_t fc = end >= kFrameDots ? 1u : 0u;
         std::uint32_t status = r8(reg::kStatus);
@@ -382,15 +390,48 @@ struct Console {
             if (crossed(kVblankDot)) {
                 if (!(status & 0x80) && (ctrl & 0x80)) flags |= kNmiPending;
                 status |= 0x80;
+                if (s.present != nullptr && (every_vblank || r32(reg::kFramesLeft) <= fo + 1))
+                    flags |= kPresentPending;   // captured after the instruction
             }
             if (crossed(kPreRenderDot)) {
                 status &= 0x1F;
                 flags &= ~kNmiPending;
+                if (s.present != nullptr) {   // frame-start scroll/ctrl of the next snapshot
+                    s.lat_sx[env] = static_cast<std::uint8_t>(r8(reg::kScrollX));
+                    s.lat_sy[env] = static_cast<std::uint8_t>(r8(reg::kScrollY));
+                    s.lat_ctrl[env] = static_cast<std::uint8_t>(ctrl);
+                }
             }
         }
         w8(reg::kStatus, status);
         w32(reg::kFrameDot, end - fc * kFrameDots);
         return fc;
+    }
+
+    // Presentation record of this console (batch_ppu.cuh:224-249): scroll and
+    // ctrl latched at the last pre-render line, the current ones, the mask,
+    // then the video memory block.  `lane`/`lanes`: the copy is shared by
+    // `lanes` cooperating lanes (1 when the console's own lane does it alone).
+    __device__ static void capture(const DeviceState& s, std::uint32_t e_env, std::uint32_t e_regs,
+                                   std::uint32_t lane, std::uint32_t lanes) {
+        const std::uint32_t vs = s.vram_stride;
+        std::uint8_t* rec = s.present + static_cast<std::size_t>(e_env) * (present::kHeader + vs);
+        for (std::uint32_t k = lane; k < 7; k += lanes) {
+            std::uint32_t v;
+            switch (k) {
+                case 0: v = s.lat_sx[e_env]; break;
+                case 1: v = s.lat_sy[e_env]; break;
+                case 2: v = s.lat_ctrl[e_env]; break;
+                case 3: v = lds[e_regs + reg::kScrollX]; break;
+                case 4: v = lds[e_regs + reg::kScrollY]; break;
+                case 5: v = lds[e_regs + reg::kCtrl]; break;
+                default: v = lds[e_regs + reg::kMask]; break;
+            }
+            rec[k] = static_cast<std::uint8_t>(v);
+        }
+        const auto* from = reinterpret_cast<const std::uint32_t*>(s.vram + static_cast<std::size_t>(e_env) * vs);
+        auto* to = reinterpret_cast<std::uint32_t*>(rec + present::kHeader);
+        for (std::uint32_t i = lane; i < vs / 4; i += lanes) to[i] = from[i];
     }
 };
 
@@ -702,7 +743,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
         }
         left -= static_cast<std::int32_t>(dots);
         if (counted && left <= 0) {  // a timing event was crossed: settle the PPU
-            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
+            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), kBudget);
             const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
             c.w32(reg::kHorizon, h);
             left = static_cast<std::int32_t>(h);
@@ -715,7 +756,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
             }
         }
         if (kBudget && counted && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
-            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left));
+            const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), true);
             const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
             c.w32(reg::kHorizon, h);
             left = static_cast<std::int32_t>(h);
@@ -739,6 +780,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
             const std::uint32_t page = lds[e_regs + reg::kDmaPage];
             const std::uint32_t oa = lds[e_regs + reg::kOamAddr];
             const std::uint32_t e_base = e_regs - C::kRegs;
+            std::uint8_t* e_oam = s.vram + static_cast<std::size_t>(e_env) * s.vram_stride + vram::kOam;
             if (page < 0x20 || page >= 0x60) {
                 for (std::uint32_t k = 0; k < 4; ++k) {
                     const std::uint32_t i = 4 * lane + k;
@@ -752,7 +794,7 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
                     } else {
                         val = lds[addr & 0x7FFF];
                     }
-                    s.oam[__umul24((oa + i) & 0xFF, P) + e_env] = static_cast<std::uint8_t>(val);
+                    e_oam[(oa + i) & 0xFF] = static_cast<std::uint8_t>(val);
                 }
             } else if (lane == src) {
                 // OAMADDR advances with every byte (ppu.hpp:131-134), which a
@@ -761,12 +803,24 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
                     const std::uint32_t at = (oa + i) & 0xFF;
                     c.w8(reg::kOamAddr, at);
                     const std::uint32_t val = c.bus_rd((page << 8) | i);
-                    s.oam[__umul24(at, P) + e_env] = static_cast<std::uint8_t>(val);
+                    e_oam[at] = static_cast<std::uint8_t>(val);
                 }
                 c.w8(reg::kOamAddr, oa);
             }
         }
         c.flags &= ~kDmaPending;
+        // Presentation snapshot at vblank (batch_ppu.cuh:219-249), after the
+        // OAM DMA of the same instruction: the wave copies one console's
+        // video memory block at a time (dwords, contiguous) into its record.
+        std::uint64_t preq = __ballot((c.flags & kPresentPending) != 0);
+        while (preq != 0) {
+            const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(preq)) - 1);
+            preq &= preq - 1;
+            const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
+            const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
+            C::capture(s, e_env, e_regs, lane, 64);
+        }
+        c.flags &= ~kPresentPending;
         // Code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through the bus,
         // in order, once the PPU has settled.
         if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
@@ -775,8 +829,11 @@ __global__ void __launch_bounds__(kMaxBlock) step_kernel(DeviceState s, std::uin
     if (!mine) return;
     // Settle the dots of instructions executed since the last event (only a
     // console that faulted stops between events).
-    if (left != static_cast<std::int32_t>(c.r32(reg::kHorizon)))
-        c.w32(reg::kFrames, c.r32(reg::kFrames) + c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left)));
+    if (left != static_cast<std::int32_t>(c.r32(reg::kHorizon))) {
+        c.w32(reg::kFrames,
+              c.r32(reg::kFrames) + c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), true));
+        if (c.flags & kPresentPending) C::capture(s, env, base + C::kRegs, 0, 1);
+    }
 
     // Write the LDS-resident RAM rows and registers back to HBM.
     {

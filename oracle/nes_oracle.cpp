@@ -28,6 +28,7 @@
 //  2128 prg_ram[8192] | 10320 oam[256] | 10576 palette[32]
 //  10608 nametable[4096] | 14704 chr_ram[8192] | 22896 end
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <chrono>
 #include <cstdint>
@@ -99,6 +100,33 @@ struct Machine {
     std::uint8_t nt[4096] = {};
     std::uint8_t palette[32] = {};
     std::uint8_t chr_ram[8192] = {};
+    // Presentation snapshot of the batched core (batch_ppu.cuh:215-260,
+    // cuda_module.cu seed_presentation_snapshot): what a rendered frame shows
+    // is frozen at every vblank (OAM, nametables, palette and end-of-frame
+    // scroll/ctrl/mask); scroll and ctrl are latched at every pre-render line
+    // and become the frame-start values of the next snapshot.
+    struct Presentation {
+        std::uint8_t sx_start = 0, sy_start = 0, ctrl_start = 0, sx_end = 0, sy_end = 0, ctrl_end = 0, mask = 0;
+        std::uint8_t oam[256] = {}, nt[4096] = {}, palette[32] = {};
+    } snap;
+    std::uint8_t lat_sx = 0, lat_sy = 0, lat_ctrl = 0;
+
+    void seed_presentation() {
+        std::memcpy(snap.oam, oam, 256);
+        std::memcpy(snap.nt, nt, 4096);
+        std::memcpy(snap.palette, palette, 32);
+        snap.mask = mask;
+        lat_sx = snap.sx_start = snap.sx_end = scroll_x;
+        lat_sy = snap.sy_start = snap.sy_end = scroll_y;
+        lat_ctrl = snap.ctrl_start = snap.ctrl_end = ctrl;
+    }
+    void capture_presentation() {
+        snap.sx_start = lat_sx; snap.sy_start = lat_sy; snap.ctrl_start = lat_ctrl;
+        snap.sx_end = scroll_x; snap.sy_end = scroll_y; snap.ctrl_end = ctrl; snap.mask = mask;
+        std::memcpy(snap.oam, oam, 256);
+        std::memcpy(snap.nt, nt, 4096);
+        std::memcpy(snap.palette, palette, 32);
+    }
 
     // ---- PPU memory (ppu.hpp:280-338) -------------------------------------
     static std::uint16_t pal_index(std::uint16_t addr) {
@@ -228,11 +256,13 @@ struct Machine {
             if (scanline == 241) {
                 if (!(status & 0x80) && (ctrl & 0x80)) nmi_pending = 1;
                 status |= 0x80;
+                capture_presentation();
             } else if (scanline == 30 && (mask & 0x18)) {
                 status |= 0x40;
             } else if (scanline == 261) {
                 status &= 0x1F;   // clears vblank, sprite 0 and overflow
                 nmi_pending = 0;
+                lat_sx = scroll_x; lat_sy = scroll_y; lat_ctrl = ctrl;
             }
         }
         return frames;
@@ -310,6 +340,7 @@ struct Machine {
         p = kU | kI;
         pc = read16(0xFFFC);
         cycles = 7;
+        seed_presentation();   // the batched core seeds it at every full reset
     }
 
     void nmi() {
@@ -568,6 +599,114 @@ struct Machine {
         return n;
     }
 
+    // ---- frame rendering (batch_render.cuh:161-440, ppu.hpp:213-230,397-545) --
+    // The state one frame is drawn from.
+    struct View {
+        std::uint8_t ctrl, mask, sx, sy;
+        const std::uint8_t *nt, *pal, *oam;
+    };
+    // Two rule sets.  `cpu`: the reference CPU core's renderer (live state,
+    // a background pixel is opaque when its pattern colour is non-zero, CHR
+    // RAM is read).  Otherwise the batched core's renderer: a background pixel
+    // counts as transparent when its palette value is 0, CHR RAM reads as 0,
+    // and the frame comes from the presentation snapshot when `snapshot`.
+    std::uint8_t ppu_view_read(const View& w, std::uint16_t addr, bool cpu) const {
+        addr &= 0x3FFF;
+        if (addr < 0x2000) {
+            if (!cart->chr.empty()) return cart->chr[addr % cart->chr.size()];
+            return cpu ? chr_ram[addr & 0x1FFF] : 0;
+        }
+        if (addr < 0x3F00) {
+            if (addr >= 0x3000) addr -= 0x1000;
+            return w.nt[nt_index(addr)];
+        }
+        return w.pal[pal_index(addr)];
+    }
+    std::uint8_t palette_value(const View& w, unsigned index, bool cpu) const {
+        std::uint8_t v = ppu_view_read(w, static_cast<std::uint16_t>(0x3F00 + index), cpu);
+        if (w.mask & 0x01) v &= 0x30;
+        return v & 0x3F;
+    }
+    unsigned pattern_colour(const View& w, unsigned tile_base, unsigned fx, unsigned fy, bool cpu) const {
+        const unsigned lo = ppu_view_read(w, static_cast<std::uint16_t>(tile_base + fy), cpu);
+        const unsigned hi = ppu_view_read(w, static_cast<std::uint16_t>(tile_base + fy + 8), cpu);
+        const unsigned bit = 7 - fx;
+        return ((lo >> bit) & 1) | (((hi >> bit) & 1) << 1);
+    }
+    // Background at (x, y): *colour = pattern colour (0 transparent), returns
+    // the palette value (0 when transparent).
+    std::uint8_t background(const View& w, unsigned x, unsigned y, unsigned* colour, bool cpu) const {
+        *colour = 0;
+        if (!(w.mask & 0x08) || (!(w.mask & 0x02) && x < 8)) return 0;
+        const unsigned wy = w.sy + y, wx = w.sx + x;
+        const unsigned coarse_y = (wy % 240) / 8, fine_y = wy & 7;
+        const unsigned base_nt = w.ctrl & 3;
+        const unsigned nt_y = ((base_nt >> 1) + wy / 240) & 1;
+        const unsigned coarse_x = (wx & 0xFF) / 8, fine_x = wx & 7;
+        const unsigned nt_x = ((base_nt & 1) + wx / 256) & 1;
+        const unsigned nt_base = 0x2000 + (nt_x | (nt_y << 1)) * 0x400;
+        const unsigned pattern_base = (w.ctrl & 0x10) ? 0x1000 : 0;
+        const unsigned tile = ppu_view_read(w, static_cast<std::uint16_t>(nt_base + coarse_y * 32 + coarse_x), cpu);
+        const unsigned c = pattern_colour(w, pattern_base + tile * 16, fine_x, fine_y, cpu);
+        if (c == 0) return 0;
+        *colour = c;
+        const unsigned attr = ppu_view_read(w, static_cast<std::uint16_t>(nt_base + 0x3C0 + (coarse_y / 4) * 8 + coarse_x / 4), cpu);
+        const unsigned shift = ((coarse_y & 2) << 1) | (coarse_x & 2);
+        return palette_value(w, ((attr >> shift) & 3) * 4 + c, cpu);
+    }
+    unsigned sprite_colour(const View& w, unsigned tile, unsigned attr, unsigned px, unsigned py, bool cpu) const {
+        if (attr & 0x40) px = 7 - px;
+        if (w.ctrl & 0x20) {
+            if (attr & 0x80) py = 15 - py;
+            const unsigned base = (tile & 1) ? 0x1000 : 0;
+            const unsigned t = ((tile & 0xFE) + py / 8) & 0xFF;
+            return pattern_colour(w, base + t * 16, px, py & 7, cpu);
+        }
+        if (attr & 0x80) py = 7 - py;
+        const unsigned base = (w.ctrl & 0x08) ? 0x1000 : 0;
+        return pattern_colour(w, base + tile * 16, px, py, cpu);
+    }
+    // One frame of palette values (0..63), 240 rows x 256.
+    void render(std::uint8_t* out, bool snapshot, bool cpu) const {
+        const View live{ctrl, mask, scroll_x, scroll_y, nt, palette, oam};
+        View play = live, hud = live;
+        int split = 0;
+        if (snapshot && !cpu) {
+            play = View{snap.ctrl_end, snap.mask, snap.sx_end, snap.sy_end, snap.nt, snap.palette, snap.oam};
+            hud = View{snap.ctrl_start, snap.mask, snap.sx_start, snap.sy_start, snap.nt, snap.palette, snap.oam};
+            split = snap.oam[0] + 1 + ((play.ctrl & 0x20) ? 16 : 8);
+            if (split >= 240) { play = hud; split = 0; }
+        }
+        for (unsigned y = 0; y < 240; ++y) {
+            for (unsigned x = 0; x < 256; ++x) {
+                unsigned c = 0;
+                const View& bs = static_cast<int>(y) < split ? hud : play;
+                const std::uint8_t bgv = background(bs, x, y, &c, cpu);
+                const bool bg_opaque = cpu ? (c != 0) : (bgv != 0);
+                std::uint8_t colour = bg_opaque ? bgv : palette_value(play, 0, cpu);
+                if ((play.mask & 0x10) && ((play.mask & 0x04) || x >= 8)) {
+                    const unsigned h = (play.ctrl & 0x20) ? 16 : 8;
+                    for (unsigned sp = 0; sp < 64; ++sp) {
+                        const int sy = static_cast<int>(y) - (play.oam[4 * sp] + 1);
+                        const int sx = static_cast<int>(x) - play.oam[4 * sp + 3];
+                        if (sy < 0 || sy >= static_cast<int>(h) || sx < 0 || sx >= 8) continue;
+                        const unsigned attr = play.oam[4 * sp + 2];
+                        if (attr & 0x20) {   // behind the background
+                            unsigned c2 = 0;
+                            const std::uint8_t v2 = background(play, x, y, &c2, cpu);
+                            if (cpu ? (c2 != 0) : (v2 != 0)) continue;
+                        }
+                        const unsigned sc = sprite_colour(play, play.oam[4 * sp + 1], attr, sx, sy, cpu);
+                        if (sc == 0) continue;
+                        colour = palette_value(play, 0x10 + (attr & 3) * 4 + sc, cpu);
+                        break;
+                    }
+                }
+                out[y * 256 + x] = colour;
+            }
+        }
+    }
+
     // ---- canonical state blob ------------------------------------------------
     void save(std::uint8_t* o) const {
         std::memset(o, 0, kStateBytes);
@@ -686,6 +825,106 @@ std::uint64_t splitmix64(std::uint64_t x) {
     return z ^ (z >> 31);
 }
 
+// ---- 84x84 grayscale --------------------------------------------------------
+// The pixel observation of the vendored project's PixelPreprocess
+// (project/mario-rl-ram/src/mario_rl/wrappers.py:209-215) applied to the
+// batched core's RGB frame (batch_render.cuh palette):
+//   gray = uint8(np.dot(float32 RGB, [0.299, 0.587, 0.114]))  -- numpy 2.2
+//     (OpenBLAS dgemv) evaluates the length-3 dot as fma(b, .114, fma(g, .587,
+//     r * .299)) in double; the cast truncates;
+//   Image.fromarray(gray).resize((84, 84), Image.BILINEAR)  -- Pillow 12's
+//     separable resample (libImaging/Resample.c): horizontal pass first into
+//     an 8-bit image, then vertical; triangle filter of support 1 widened by
+//     the scale, weights normalised and rounded to 22-bit fixed point, each
+//     output = clip8((2^21 + sum in * w) >> 22).
+constexpr std::uint8_t kNesRgb[192] = {
+    0x54, 0x54, 0x54, 0x00, 0x1E, 0x74, 0x08, 0x10, 0x90, 0x30, 0x00, 0x88,
+    0x44, 0x00, 0x64, 0x5C, 0x00, 0x30, 0x54, 0x04, 0x00, 0x3C, 0x18, 0x00,
+    0x20, 0x2A, 0x00, 0x08, 0x3A, 0x00, 0x00, 0x40, 0x00, 0x00, 0x3C, 0x00,
+    0x00, 0x32, 0x3C, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00,
+    0x98, 0x96, 0x98, 0x08, 0x4C, 0xC4, 0x30, 0x32, 0xEC, 0x5C, 0x1E, 0xE4,
+    0x88, 0x14, 0xB0, 0xA0, 0x14, 0x64, 0x98, 0x22, 0x20, 0x78, 0x3C, 0x00,
+    0x54, 0x5A, 0x00, 0x28, 0x72, 0x00, 0x08, 0x7C, 0x00, 0x00, 0x76, 0x28,
+    0x00, 0x66, 0x78, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00,
+    0xEC, 0xEE, 0xEC, 0x4C, 0x9A, 0xEC, 0x78, 0x7C, 0xEC, 0xB0, 0x62, 0xEC,
+    0xE4, 0x54, 0xEC, 0xEC, 0x58, 0xB4, 0xEC, 0x6A, 0x64, 0xD4, 0x88, 0x20,
+    0xA0, 0xAA, 0x00, 0x74, 0xC4, 0x00, 0x4C, 0xD0, 0x20, 0x38, 0xCC, 0x6C,
+    0x38, 0xB4, 0xCC, 0x3C, 0x3C, 0x3C, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00,
+    0xEC, 0xEE, 0xEC, 0xA8, 0xCC, 0xEC, 0xBC, 0xBC, 0xEC, 0xD4, 0xB2, 0xEC,
+    0xEC, 0xAE, 0xEC, 0xEC, 0xAE, 0xD4, 0xEC, 0xB4, 0xB0, 0xE4, 0xC4, 0x90,
+    0xCC, 0xD2, 0x78, 0xB4, 0xDE, 0x78, 0xA8, 0xE2, 0x90, 0x98, 0xE2, 0xB4,
+    0xA0, 0xD6, 0xE4, 0xA0, 0xA2, 0xA0, 0x00, 0x00, 0x00, 0x00, 0x00, 0x00,
+};
+
+std::uint8_t gray_of(unsigned index) {
+    const double r = kNesRgb[3 * index], g = kNesRgb[3 * index + 1], b = kNesRgb[3 * index + 2];
+    return static_cast<std::uint8_t>(static_cast<int>(std::fma(b, 0.114, std::fma(g, 0.587, r * 0.299))));
+}
+
+struct Resample {
+    int ksize = 0;
+    std::vector<int> lo, n, k;   // per output: first input, input count, ksize weights
+};
+
+Resample pil_bilinear(int in_size, int out_size) {
+    constexpr int kPrecision = 22;
+    Resample rs;
+    const double scale = static_cast<double>(in_size) / out_size;
+    const double filterscale = scale < 1.0 ? 1.0 : scale;
+    const double support = 1.0 * filterscale;
+    rs.ksize = static_cast<int>(std::ceil(support)) * 2 + 1;
+    rs.k.assign(static_cast<std::size_t>(out_size * rs.ksize), 0);
+    for (int xx = 0; xx < out_size; ++xx) {
+        const double center = (xx + 0.5) * scale;
+        const double ss = 1.0 / filterscale;
+        int xmin = static_cast<int>(center - support + 0.5);
+        if (xmin < 0) xmin = 0;
+        int xmax = static_cast<int>(center + support + 0.5);
+        if (xmax > in_size) xmax = in_size;
+        xmax -= xmin;
+        std::vector<double> w(static_cast<std::size_t>(xmax));
+        double ww = 0.0;
+        for (int x = 0; x < xmax; ++x) {
+            double t = (x + xmin - center + 0.5) * ss;
+            if (t < 0.0) t = -t;
+            w[x] = t < 1.0 ? 1.0 - t : 0.0;
+            ww += w[x];
+        }
+        for (int x = 0; x < xmax; ++x) {
+            if (ww != 0.0) w[x] /= ww;
+            rs.k[xx * rs.ksize + x] = w[x] < 0 ? static_cast<int>(-0.5 + w[x] * (1 << kPrecision))
+                                              : static_cast<int>(0.5 + w[x] * (1 << kPrecision));
+        }
+        rs.lo.push_back(xmin);
+        rs.n.push_back(xmax);
+    }
+    return rs;
+}
+
+std::uint8_t clip8(std::int64_t v) {
+    v >>= 22;
+    return static_cast<std::uint8_t>(v < 0 ? 0 : (v > 255 ? 255 : v));
+}
+
+// 240x256 palette values -> 84x84 gray.
+void gray84(const std::uint8_t* frame, std::uint8_t* out) {
+    static const Resample h = pil_bilinear(256, 84), v = pil_bilinear(240, 84);
+    std::vector<std::uint8_t> gray(240 * 256), mid(240 * 84);
+    for (int i = 0; i < 240 * 256; ++i) gray[i] = gray_of(frame[i] & 0x3F);
+    for (int y = 0; y < 240; ++y)
+        for (int x = 0; x < 84; ++x) {
+            std::int64_t acc = 1 << 21;
+            for (int j = 0; j < h.n[x]; ++j) acc += static_cast<std::int64_t>(gray[y * 256 + h.lo[x] + j]) * h.k[x * h.ksize + j];
+            mid[y * 84 + x] = clip8(acc);
+        }
+    for (int y = 0; y < 84; ++y)
+        for (int x = 0; x < 84; ++x) {
+            std::int64_t acc = 1 << 21;
+            for (int j = 0; j < v.n[y]; ++j) acc += static_cast<std::int64_t>(mid[(v.lo[y] + j) * 84 + x]) * v.k[y * v.ksize + j];
+            out[y * 84 + x] = clip8(acc);
+        }
+}
+
 struct Env {
     Cart cart;
     Machine m;
@@ -788,6 +1027,23 @@ void oracle_load(void* h, const std::uint8_t* in) {
 }
 
 std::uint64_t oracle_fnv1a(const std::uint8_t* d, std::size_t n) { return fnv1a(d, n); }
+
+// One frame of palette values (240 x 256).  mode bit 0: from the presentation
+// snapshot (batched core); bit 1: the CPU core's renderer rules (live state).
+void oracle_render(void* h, std::uint32_t mode, std::uint8_t* out) {
+    static_cast<Env*>(h)->m.render(out, (mode & 1) != 0, (mode & 2) != 0);
+}
+// Re-seed the presentation snapshot from live state (a full reset does this).
+void oracle_seed_presentation(void* h) { static_cast<Env*>(h)->m.seed_presentation(); }
+// Overwrite the snapshot's scroll/ctrl/mask: start x, start y, start ctrl,
+// end x, end y, end ctrl, mask (test hook for the HUD/play split).
+void oracle_set_presentation(void* h, const std::uint8_t* f) {
+    auto& p = static_cast<Env*>(h)->m.snap;
+    p.sx_start = f[0]; p.sy_start = f[1]; p.ctrl_start = f[2];
+    p.sx_end = f[3]; p.sy_end = f[4]; p.ctrl_end = f[5]; p.mask = f[6];
+}
+void oracle_palette_rgb(std::uint8_t* out) { std::memcpy(out, kNesRgb, sizeof(kNesRgb)); }
+void oracle_gray84(const std::uint8_t* frame, std::uint8_t* out) { gray84(frame, out); }
 std::uint64_t oracle_splitmix64(std::uint64_t x) { return splitmix64(x); }
 
 // CPU baseline: n_envs consoles, each on its own controller stream

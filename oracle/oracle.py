@@ -113,6 +113,11 @@ def _oracle_lib():
         lib.oracle_fnv1a.argtypes = [_U8P, ctypes.c_size_t]
         lib.oracle_splitmix64.restype = ctypes.c_uint64
         lib.oracle_splitmix64.argtypes = [ctypes.c_uint64]
+        lib.oracle_render.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _U8P]
+        lib.oracle_seed_presentation.argtypes = [ctypes.c_void_p]
+        lib.oracle_set_presentation.argtypes = [ctypes.c_void_p, _U8P]
+        lib.oracle_palette_rgb.argtypes = [_U8P]
+        lib.oracle_gray84.argtypes = [_U8P, _U8P]
         lib.oracle_run_batch.restype = ctypes.c_double
         lib.oracle_run_batch.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,
@@ -139,6 +144,7 @@ def _ref_lib():
         lib.ref_load.argtypes = [ctypes.c_void_p, _U8P]
         lib.ref_step_instruction.restype = ctypes.c_int64
         lib.ref_step_instruction.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
+        lib.ref_render_rgb.argtypes = [ctypes.c_void_p, _U8P]
         lib.ref_run_batch.restype = ctypes.c_double
         lib.ref_run_batch.argtypes = _oracle_lib().oracle_run_batch.argtypes
         _REF = lib
@@ -203,6 +209,22 @@ class Oracle:
         assert st.size == STATE_BYTES
         self.lib.oracle_load(self.h, st.ctypes.data_as(_U8P))
 
+    def render(self, snapshot: bool = True, cpu_rules: bool = False) -> np.ndarray:
+        """Palette values (240, 256): the batched core's frame from the
+        presentation snapshot, or from live state; `cpu_rules` follows the
+        reference CPU core's renderer instead (live state)."""
+        out = np.empty((240, 256), dtype=np.uint8)
+        self.lib.oracle_render(self.h, (1 if snapshot else 0) | (2 if cpu_rules else 0), out.ctypes.data_as(_U8P))
+        return out
+
+    def seed_presentation(self) -> None:
+        self.lib.oracle_seed_presentation(self.h)
+
+    def set_presentation(self, sx_start: int, sy_start: int, ctrl_start: int, sx_end: int, sy_end: int,
+                         ctrl_end: int, mask: int) -> None:
+        f = np.array([sx_start, sy_start, ctrl_start, sx_end, sy_end, ctrl_end, mask], dtype=np.uint8)
+        self.lib.oracle_set_presentation(self.h, f.ctypes.data_as(_U8P))
+
 
 class RefConsole:
     """One console of the reference's own CPU core (oracle/_ref)."""
@@ -240,6 +262,28 @@ class RefConsole:
         st = np.ascontiguousarray(state, dtype=np.uint8)
         assert st.size == STATE_BYTES
         self.lib.ref_load(self.h, st.ctypes.data_as(_U8P))
+
+    def render_rgb(self) -> np.ndarray:
+        """The reference CPU core's frame (240, 256, 3) (ppu.hpp:213-230)."""
+        out = np.empty((240, 256, 3), dtype=np.uint8)
+        self.lib.ref_render_rgb(self.h, out.ctypes.data_as(_U8P))
+        return out
+
+
+def palette_rgb() -> np.ndarray:
+    """The 64-entry NES palette (64, 3) of the batched core's renderer."""
+    out = np.empty((64, 3), dtype=np.uint8)
+    _oracle_lib().oracle_palette_rgb(out.ctypes.data_as(_U8P))
+    return out
+
+
+def gray84(frame: np.ndarray) -> np.ndarray:
+    """Palette values (240, 256) -> the 84x84 gray observation (restated)."""
+    f = np.ascontiguousarray(frame, dtype=np.uint8)
+    assert f.shape == (240, 256)
+    out = np.empty((84, 84), dtype=np.uint8)
+    _oracle_lib().oracle_gray84(f.ctypes.data_as(_U8P), out.ctypes.data_as(_U8P))
+    return out
 
 
 def run_batch(rom: bytes, num_envs: int, steps: int, frameskip: int, seed: int, threads: int,

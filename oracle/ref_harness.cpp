@@ -76,6 +76,12 @@ void* ref_create(const std::uint8_t* ines, std::size_t len) {
 
 void ref_destroy(void* h) { delete static_cast<RefEnv*>(h); }
 
+// The reference CPU core's frame (ppu.hpp:213-230): 240 x 256 x RGB.
+void ref_render_rgb(void* h, std::uint8_t* out) {
+    const auto frame = static_cast<RefEnv*>(h)->console.ppu().render_rgb_frame();
+    std::memcpy(out, frame.data(), frame.size());
+}
+
 std::int64_t ref_step(void* h, std::uint8_t buttons, std::uint32_t frameskip, std::uint64_t max_instructions) {
     auto* e = static_cast<RefEnv*>(h);
     try {
