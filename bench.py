@@ -7,7 +7,10 @@ step's 4 frames); done fires when the ROM's countdown byte reaches 0 and the
 console auto-resets from one of 8 snapshots captured after 100-800 seeded
 warm-up frames (per-env level drawn uniformly); reward = clip(dx, -15, 15) -
 0.01 on the ROM's 16-bit x position.  The 4,096-console configuration (no
-resets) is timed in the same run and reported under "extra".
+resets) is timed in the same run and reported under "extra", and so is the
+pixel-observation workload: 16,384 consoles, each step followed by one render
+of every console's 84x84 gray observation into device memory (100 steps by
+default; the full 2,000 take ``--pixel-steps 2000``).
 
 Timed region: W untimed warm-up steps, synchronize, K timed steps of the
 Python-level ``CudaBatch.step_device(actions[k], auto_reset=True)`` loop (the
@@ -100,7 +103,7 @@ def make_snapshots(core, rom: bytes, rng: np.random.Generator) -> tuple[list[byt
 
 
 def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots: list[bytes] | None,
-            levels: np.ndarray | None) -> dict:
+            levels: np.ndarray | None, gray84: bool = False) -> dict:
     import torch
 
     reward = {"kind": "x_delta", "x_lo": synthrom.X_LO, "x_hi": synthrom.X_HI,
@@ -115,12 +118,16 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
     torch.cuda.synchronize()
     for k in range(warmup):
         out = batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
+        if gray84:
+            batch.render_frames_device(rgb=False, palette=False, gray84=True)
     torch.cuda.synchronize()
     batch.set_timing(True)
     done_total = 0
     t0 = time.perf_counter()
     for k in range(warmup, warmup + steps):
         out = batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
+        if gray84:
+            batch.render_frames_device(rgb=False, palette=False, gray84=True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernel_ms, launches = batch.kernel_timing()
@@ -204,6 +211,8 @@ def main() -> int:
     ap.add_argument("--envs", type=int, default=65536)
     ap.add_argument("--small-envs", type=int, default=4096)
     ap.add_argument("--small-steps", type=int, default=200)
+    ap.add_argument("--pixel-envs", type=int, default=16384)
+    ap.add_argument("--pixel-steps", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -236,6 +245,12 @@ def main() -> int:
     log(f"timing {args.small_envs} envs x {args.small_steps} steps (no resets)")
     small = run_gpu(core, rom, args.small_envs, args.small_steps, max(5, args.warmup // 4), None, None)
     log(f"  {small['env_steps_per_s']:.0f} env-steps/s")
+    pixel = None
+    if args.pixel_steps > 0:
+        log(f"timing {args.pixel_envs} envs x {args.pixel_steps} steps with an 84x84 gray frame per step")
+        pixel = run_gpu(core, rom, args.pixel_envs, args.pixel_steps, max(5, args.warmup // 4), None, None,
+                        gray84=True)
+        log(f"  {pixel['env_steps_per_s']:.0f} env-steps/s (pixel observations)")
 
     kernel_s = big["kernel_ms_per_launch"] / 1000.0
     hbm_achieved = args.envs * B_STEP / kernel_s / 1e9
@@ -280,7 +295,7 @@ def main() -> int:
             "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
         },
-        "extra": {"envs_4096": small, "envs_65536": big},
+        "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")

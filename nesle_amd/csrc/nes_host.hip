@@ -226,7 +226,7 @@ struct nesle_batch {
     std::uint8_t* d_frame_rgb = nullptr;
     std::uint8_t* d_frame_palette = nullptr;
     std::uint8_t* d_gray84 = nullptr;
-    void* d_render_tables = nullptr;   // render::Taps, then the 64-entry gray LUT
+    void* d_render_tables = nullptr;   // render::Tables
     // Step-kernel timing: event pairs are recorded per launch and folded into
     // the totals once the pair has completed.
     bool timing = false;
@@ -335,12 +335,9 @@ struct nesle_batch {
 
     void ensure_render_tables() {
         if (d_render_tables != nullptr) return;
-        const nesle::render::Taps taps = nesle::render::make_taps();
-        std::vector<std::uint8_t> host(sizeof(taps) + 64);
-        std::memcpy(host.data(), &taps, sizeof(taps));
-        nesle::render::make_gray_lut(host.data() + sizeof(taps));
-        hip_check(hipMalloc(&d_render_tables, host.size()), "hipMalloc render tables");
-        host_to_device(d_render_tables, host.data(), host.size(), "upload render tables");
+        const nesle::render::Tables t = nesle::render::make_tables();
+        hip_check(hipMalloc(&d_render_tables, sizeof(t)), "hipMalloc render tables");
+        host_to_device(d_render_tables, &t, sizeof(t), "upload render tables");
     }
 
     std::pair<hipEvent_t, hipEvent_t> take_events() {
@@ -677,8 +674,7 @@ int nesle_render(nesle_batch* b, std::uint32_t outputs) {
         a.chr = b->rom.chr.empty() ? nullptr : b->d_chr;
         a.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
         a.nt_mode = b->ds.nt_mode;
-        a.taps = static_cast<const nesle::render::Taps*>(b->d_render_tables);
-        a.gray_lut = static_cast<const std::uint8_t*>(b->d_render_tables) + sizeof(nesle::render::Taps);
+        a.tables = static_cast<const nesle::render::Tables*>(b->d_render_tables);
         a.rgb = (outputs & NESLE_FRAME_RGB) ? b->frame_buffer(NESLE_FRAME_RGB) : nullptr;
         a.palette = (outputs & NESLE_FRAME_PALETTE) ? b->frame_buffer(NESLE_FRAME_PALETTE) : nullptr;
         a.gray = (outputs & NESLE_FRAME_GRAY84) ? b->frame_buffer(NESLE_FRAME_GRAY84) : nullptr;

@@ -19,14 +19,18 @@ struct Taps {
     std::int32_t v_lo[kOut], v_n[kOut], v_k[kOut][kVTaps];
 };
 
-// Host: the resize weights of Pillow's BILINEAR filter for 256x240 -> 84x84
-// (libImaging/Resample.c precompute_coeffs + normalize_coeffs_8bpc).
-Taps make_taps();
-// Host: gray value of each of the 64 palette colours, uint8(fma(b, .114,
-// fma(g, .587, r * .299))) -- numpy's float luma of the RGB frame, truncated.
-void make_gray_lut(std::uint8_t* lut);
-// Host: the renderer's RGB palette (64 x 3).
-const std::uint8_t* nes_rgb();
+// Everything the render kernel looks up, uploaded once per batch.
+struct Tables {
+    Taps taps;               // Pillow BILINEAR weights for 256x240 -> 84x84
+    std::uint8_t gray[64];   // gray level of each palette colour
+    std::uint8_t rgb[192];   // the renderer's RGB palette (64 x 3)
+};
+
+// Host: the resize weights of Pillow's BILINEAR filter (libImaging/Resample.c
+// precompute_coeffs + normalize_coeffs_8bpc), the gray level of each palette
+// colour, uint8(fma(b, .114, fma(g, .587, r * .299))) -- numpy's float luma of
+// the RGB frame, truncated -- and the RGB palette.
+Tables make_tables();
 
 }  // namespace render
 
@@ -37,8 +41,7 @@ struct RenderArgs {
     const std::uint8_t* chr;         // CHR ROM (device), null for CHR RAM
     std::uint32_t chr_size;          // 0 for CHR RAM
     std::uint32_t nt_mode;           // 0 vertical, 1 horizontal, 2 four-screen
-    const std::uint8_t* gray_lut;    // [64] (device)
-    const render::Taps* taps;        // (device)
+    const render::Tables* tables;    // (device)
     std::uint8_t* palette;           // [n][240][256] or null
     std::uint8_t* rgb;               // [n][240][256][3] or null
     std::uint8_t* gray;              // [n][84][84] or null
