@@ -47,8 +47,14 @@ struct View {
     std::uint32_t ctrl, sx, sy;
 };
 
-// Reverse the bit order of a byte (horizontally flipped sprite rows).
+// Reverse the bit order of a byte (pattern rows are stored leftmost pixel in bit 7).
 __device__ __forceinline__ std::uint32_t rev8(std::uint32_t b) { return __builtin_bitreverse32(b) >> 24; }
+// Bits 0-7 of b to the even bits 0, 2, ..., 14.
+__device__ __forceinline__ std::uint32_t spread(std::uint32_t b) {
+    b = (b | (b << 4)) & 0x0F0Fu;
+    b = (b | (b << 2)) & 0x3333u;
+    return (b | (b << 1)) & 0x5555u;
+}
 
 struct Console {
     const std::uint8_t* chr;   // LDS, 8 KB pattern tables
@@ -56,7 +62,9 @@ struct Console {
     const std::uint8_t* oam;   // LDS, snapshot OAM
     const std::uint8_t* pv;    // LDS, 32 palette values (aliases and grayscale applied)
     std::uint32_t mask;
-    std::uint32_t phys[4];     // nametable 0-3 -> offset in nametable RAM (mirroring)
+    // Nametable n = x | y << 1 lives at (x * mx + y * my) * 0x400 of nametable
+    // RAM: vertical mirroring mx = 1, my = 0; horizontal 0, 1; four-screen 1, 2.
+    std::uint32_t mx, my;
 
     // Background of pixels x0..x0+7 of row y: palette values (0 = transparent)
     // packed 8 bits per pixel, two words.  batch_background_color
@@ -74,27 +82,28 @@ struct Console {
             const std::uint32_t wt = (wx0 >> 3) + k;                  // world tile column 0..63
             const std::uint32_t coarse_x = wt & 31;
             const std::uint32_t nt_x = ((w.ctrl & 1) + (wt >> 5)) & 1;
-            const std::uint8_t* n = nt + phys[nt_x | (nt_y << 1)];
+            const std::uint8_t* n = nt + (nt_x * mx + nt_y * my) * 0x400;
             const std::uint32_t tile = n[coarse_y * 32 + coarse_x];
             const std::uint32_t lo = chr[(pbase + tile * 16 + fine_y) & 0x1FFF];
             const std::uint32_t hi = chr[(pbase + tile * 16 + fine_y + 8) & 0x1FFF];
             const std::uint32_t attr = n[0x3C0 + (coarse_y >> 2) * 8 + (coarse_x >> 2)];
             const std::uint32_t shift = ((coarse_y & 2) << 1) | (coarse_x & 2);
-            // Interleave the planes: pixel j of the tile at bits 2j..2j+1 (MSB first).
-            std::uint32_t t = 0;
-            for (std::uint32_t j = 0; j < 8; ++j)
-                t |= (((lo >> (7 - j)) & 1) | (((hi >> (7 - j)) & 1) << 1)) << (2 * j);
-            planes |= t << (16 * k);
+            // Interleave the planes: pixel j of the tile (bit 7 - j of each
+            // plane) at bits 2j..2j+1.
+            planes |= (spread(rev8(lo)) | (spread(rev8(hi)) << 1)) << (16 * k);
             pal |= ((attr >> shift) & 3) << (2 * k);
         }
+        // The 4 palette values of each tile's attribute, colour 0 cleared
+        // (transparent); pixel i of the run is pixel fx + i of the pair.
+        const std::uint32_t* pw = reinterpret_cast<const std::uint32_t*>(pv);
+        const std::uint32_t p0 = pw[pal & 3] & ~0xFFu, p1 = pw[(pal >> 2) & 3] & ~0xFFu;
+        const std::uint32_t run = planes >> (2 * fx);
         for (std::uint32_t i = 0; i < 8; ++i) {
-            const std::uint32_t j = fx + i;   // 0..14 across the two tiles
-            const std::uint32_t c = (planes >> (2 * j)) & 3;
-            const std::uint32_t sel = (pal >> (j >= 8 ? 2 : 0)) & 3;
-            std::uint32_t v = c != 0 ? pv[sel * 4 + c] : 0u;
-            if (!(mask & 0x02) && x0 + i < 8) v = 0;
+            const std::uint32_t c = (run >> (2 * i)) & 3;
+            const std::uint32_t v = ((i + fx < 8 ? p0 : p1) >> (8 * c)) & 0xFF;
             out[i >> 2] |= v << (8 * (i & 3));
         }
+        if (!(mask & 0x02) && x0 == 0) out[0] = out[1] = 0;   // left 8 pixels hidden
     }
 };
 
@@ -114,7 +123,7 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
     __shared__ __attribute__((aligned(16))) std::uint8_t gband[kBand][256];
     __shared__ std::uint8_t mid[kRing][render::kOut];
     __shared__ __attribute__((aligned(16))) render::Tables tab;
-    __shared__ std::uint8_t pv[32];
+    __shared__ __attribute__((aligned(4))) std::uint8_t pv[32];
 
     const std::uint32_t tid = threadIdx.x, env = blockIdx.x;
     {
@@ -159,12 +168,23 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
     }
     __syncthreads();
 
-    Console con{chr, rec + present::kNametable, oam, pv, mask, {}};
-    for (std::uint32_t k = 0; k < 4; ++k)
-        con.phys[k] = a.nt_mode == 2 ? k * 0x400u : a.nt_mode == 0 ? (k & 1) * 0x400u : (k >> 1) * 0x400u;
+    Console con{chr, rec + present::kNametable, oam, pv, mask, a.nt_mode == 1 ? 0u : 1u,
+                a.nt_mode == 2 ? 2u : a.nt_mode == 1 ? 1u : 0u};
     const std::uint32_t r = tid >> 5, x0 = (tid & 31) * 8;
     const std::uint32_t backdrop = pv[0];
     std::uint32_t next_oy = 0;   // first gray row not yet written
+    // Horizontal resample: thread t < 252 owns output column t % 84 for band
+    // rows t / 84, +3, +6, with that column's weights in registers (taps past
+    // the window's end carry weight 0 and read inside the row).
+    const std::uint32_t h_rows = tid < 3 * render::kOut ? 1u : 0u;
+    const std::uint32_t h_ox = tid % render::kOut, h_r0 = tid / render::kOut;
+    std::int32_t h_k[render::kHTaps];
+    std::uint32_t h_lo = tab.taps.h_lo[h_ox];
+    if (h_lo + render::kHTaps > 256) h_lo = 256 - render::kHTaps;
+    for (std::uint32_t j = 0; j < render::kHTaps; ++j) {
+        const std::int32_t k = static_cast<std::int32_t>(j + h_lo) - tab.taps.h_lo[h_ox];   // tap index of input h_lo + j
+        h_k[j] = (k >= 0 && k < tab.taps.h_n[h_ox]) ? tab.taps.h_k[h_ox][k] : 0;
+    }
     for (std::uint32_t y0 = 0; y0 < 240; y0 += kBand) {
         const std::uint32_t y = y0 + r;
         const bool upper = static_cast<std::int32_t>(y) < split;
@@ -239,13 +259,11 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
             *reinterpret_cast<uint2*>(&gband[r][x0]) = make_uint2(g[0], g[1]);
         }
         __syncthreads();
-        if (a.gray) {   // horizontal pass of the band: 8 rows x 84 columns
-            for (std::uint32_t i = tid; i < kBand * render::kOut; i += kThreads) {
-                const std::uint32_t rr = i / render::kOut, ox = i % render::kOut;
+        if (a.gray && h_rows != 0) {   // horizontal pass of the band: column h_ox of rows h_r0, +3, +6
+            for (std::uint32_t rr = h_r0; rr < kBand; rr += 3) {
                 std::int32_t acc = 1 << (render::kPrecision - 1);
-                const std::uint32_t lo = tab.taps.h_lo[ox], n = tab.taps.h_n[ox];
-                for (std::uint32_t j = 0; j < n; ++j) acc += gband[rr][lo + j] * tab.taps.h_k[ox][j];
-                mid[(y0 + rr) % kRing][ox] = static_cast<std::uint8_t>(clip8(acc));
+                for (std::uint32_t j = 0; j < render::kHTaps; ++j) acc += gband[rr][h_lo + j] * h_k[j];
+                mid[(y0 + rr) % kRing][h_ox] = static_cast<std::uint8_t>(clip8(acc));
             }
         }
         __syncthreads();
