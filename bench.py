@@ -10,7 +10,10 @@ warm-up frames (per-env level drawn uniformly); reward = clip(dx, -15, 15) -
 resets) is timed in the same run and reported under "extra", and so is the
 pixel-observation workload: 16,384 consoles, each step followed by one render
 of every console's 84x84 gray observation into device memory (100 steps by
-default; the full 2,000 take ``--pixel-steps 2000``).
+default; the full 2,000 take ``--pixel-steps 2000``), and the GPU-resident PPO
+workload: 8,192 consoles x 128 steps per update on the snapshot/x-delta setup,
+RAM MLP policy (12-way action space, Xavier init), GAE and 4 epochs of
+minibatch 8,192, with the step kernel's share of the update's wall time.
 
 Timed region: W untimed warm-up steps, synchronize, K timed steps of the
 Python-level ``CudaBatch.step_device(actions[k], auto_reset=True)`` loop (the
@@ -150,6 +153,37 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
     }
 
 
+def run_ppo(rom: bytes, snapshots: list[bytes], updates: int) -> dict:
+    """GPU-resident PPO on the snapshot/x-delta setup: 8,192 consoles x 128
+    steps per update, MLP on RAM, 12-way action space, Xavier init, GAE
+    (0.99, 0.95), 4 epochs of minibatch 8,192.  Figures are the last update's
+    (the first also pays library warm-up)."""
+    from nesle_amd import native_ppo as P
+
+    n = 8192
+    reward = {"kind": "x_delta", "x_lo": synthrom.X_LO, "x_hi": synthrom.X_HI,
+              "done_addr": synthrom.DONE_BYTE, "clip": 15, "time_penalty": TIME_PENALTY}
+    levels = np.random.default_rng(SNAPSHOT_SEED + 1).integers(0, NUM_LEVELS, n)
+    cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, total_timesteps=n * 128 * updates, n_steps=128,
+                            batch_size=8192, update_epochs=4, frameskip=4, action_space="complex", init="xavier",
+                            reward=reward, save_checkpoints=False, seed=1, log_interval=1000,
+                            env_to_level=tuple(int(x) for x in levels))
+    import contextlib
+
+    with contextlib.redirect_stdout(sys.stderr):   # stdout carries only the result line
+        stats = P.train_native_ppo(cfg, rom_bytes=rom, snapshot_bytes=snapshots)
+    last = stats["per_update"][-1]
+    wall = last["rollout_s"] + last["update_s"]
+    return {
+        "num_envs": n, "n_steps": 128, "updates": stats["updates"],
+        "rollout_s": last["rollout_s"], "update_s": last["update_s"], "emulator_s": last["emulator_s"],
+        "env_steps_per_s": n * 128 / wall,
+        "rollout_env_steps_per_s": n * 128 / last["rollout_s"],
+        "emulator_share": last["emulator_s"] / wall,
+        "episodes": stats["log"][-1]["episodes"],
+    }
+
+
 def cpu_baseline(rom: bytes, target_seconds: float) -> dict | None:
     try:
         from oracle import oracle as O
@@ -213,6 +247,8 @@ def main() -> int:
     ap.add_argument("--small-steps", type=int, default=200)
     ap.add_argument("--pixel-envs", type=int, default=16384)
     ap.add_argument("--pixel-steps", type=int, default=100)
+    ap.add_argument("--ppo-updates", type=int, default=2,
+                    help="PPO updates of 8,192 consoles x 128 steps (the first warms up; 0 skips)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -245,6 +281,11 @@ def main() -> int:
     log(f"timing {args.small_envs} envs x {args.small_steps} steps (no resets)")
     small = run_gpu(core, rom, args.small_envs, args.small_steps, max(5, args.warmup // 4), None, None)
     log(f"  {small['env_steps_per_s']:.0f} env-steps/s")
+    ppo = None
+    if args.ppo_updates > 0:
+        log(f"PPO: 8192 envs x 128 steps, {args.ppo_updates} updates")
+        ppo = run_ppo(rom, snaps, args.ppo_updates)
+        log(f"  {ppo['env_steps_per_s']:.0f} env-steps/s end to end, emulator share {ppo['emulator_share']:.2f}")
     pixel = None
     if args.pixel_steps > 0:
         log(f"timing {args.pixel_envs} envs x {args.pixel_steps} steps with an 84x84 gray frame per step")
@@ -295,7 +336,7 @@ def main() -> int:
             "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
         },
-        "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel},
+        "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel, "ppo_8192x128": ppo},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")

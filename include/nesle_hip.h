@@ -131,7 +131,8 @@ void nesle_release(nesle_batch* b);
 int nesle_reset(nesle_batch* b);
 
 /* Masked reset; mask is num_envs bytes on host or device.  Replaces
- * reset_envs(mask) (cuda_module.cu:917-937). */
+ * reset_envs(mask) (cuda_module.cu:917-937).  With a device mask the call
+ * only enqueues work on the batch's stream (no synchronisation). */
 int nesle_reset_envs(nesle_batch* b, const uint8_t* mask, int mask_on_device);
 
 /* Controller masks for the next step: num_envs uint8 masks or int64 values

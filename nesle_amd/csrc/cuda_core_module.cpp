@@ -185,6 +185,31 @@ std::uintptr_t device_actions(const py::object& obj, std::uint32_t n, int* dtype
     return iface["data"].cast<py::tuple>()[0].cast<std::uintptr_t>();
 }
 
+// Device pointer of a one-byte-per-env tensor (uint8 or bool) of shape (n,).
+std::uintptr_t device_bytes(const py::object& obj, std::uint32_t n, int* dtype) {
+    *dtype = NESLE_DTYPE_U8;
+    if (py::hasattr(obj, "data_ptr") && py::hasattr(obj, "is_cuda")) {
+        if (!obj.attr("is_cuda").cast<bool>()) throw py::value_error("expected a CUDA tensor, got a CPU tensor");
+        if (py::hasattr(obj, "is_contiguous") && !obj.attr("is_contiguous")().cast<bool>())
+            throw py::value_error("mask tensor must be contiguous");
+        const auto shape = obj.attr("shape").cast<py::tuple>();
+        if (shape.size() != 1 || shape[0].cast<std::uint32_t>() != n)
+            throw py::value_error("mask tensor must have shape (" + std::to_string(n) + ",)");
+        const auto dt = py::str(obj.attr("dtype")).cast<std::string>();
+        if (dt != "torch.uint8" && dt != "torch.bool") throw py::value_error("mask tensor must be uint8 or bool");
+        return obj.attr("data_ptr")().cast<std::uintptr_t>();
+    }
+    if (!py::hasattr(obj, "__cuda_array_interface__"))
+        throw py::value_error("expected a CUDA tensor/array exposing __cuda_array_interface__");
+    const py::dict iface = obj.attr("__cuda_array_interface__").cast<py::dict>();
+    const auto shape = iface["shape"].cast<py::tuple>();
+    if (shape.size() != 1 || shape[0].cast<std::uint32_t>() != n)
+        throw py::value_error("mask array must have shape (" + std::to_string(n) + ",)");
+    const auto ts = iface["typestr"].cast<std::string>();
+    if (ts != "|u1" && ts != "<u1" && ts != "|b1") throw py::value_error("mask array must be uint8 or bool");
+    return iface["data"].cast<py::tuple>()[0].cast<std::uintptr_t>();
+}
+
 struct RewardSpec {
     std::uint32_t kind = NESLE_REWARD_SMB, x_lo = 0x86, x_hi = 0x6D, done_addr = 0, clip = 15;
     float time_penalty = 0.0f;
@@ -299,7 +324,12 @@ public:
         const auto ptr = device_actions(actions, n_, &dtype);
         check(nesle_set_actions(h_, reinterpret_cast<const void*>(ptr), dtype, 1));
         check(nesle_step(h_, auto_reset ? 1 : 0, 0));
-        if (synchronize || auto_reset) check(nesle_synchronize(h_));
+        // The action copy, the step and the fused reset are ordered on the
+        // batch's stream, so only an explicit request synchronises (the
+        // reference also synchronises after every auto-reset step,
+        // cuda_module.cu:594-600, to keep its host action copy from racing
+        // the reset kernel).
+        if (synchronize) check(nesle_synchronize(h_));
         py::dict out;
         out["rewards"] = view(NESLE_VIEW_REWARDS);
         out["dones"] = view(NESLE_VIEW_DONES);
@@ -332,6 +362,14 @@ public:
         if (v.ndim != 1 || static_cast<std::uint32_t>(v.shape[0]) != n_)
             throw py::value_error("mask must have shape (num_envs,)");
         check(nesle_reset_envs(h_, static_cast<const std::uint8_t*>(v.ptr), 0));
+    }
+
+    // Masked reset from a device mask (torch tensor or __cuda_array_interface__
+    // object, uint8/bool, shape (num_envs,)), enqueued on the batch's stream.
+    void reset_envs_device(const py::object& mask) {
+        int dtype = NESLE_DTYPE_U8;
+        const auto ptr = device_bytes(mask, n_, &dtype);
+        check(nesle_reset_envs(h_, reinterpret_cast<const std::uint8_t*>(ptr), 1));
     }
 
     void poke_ram(std::uint16_t address, std::uint8_t value) { check(nesle_poke_ram(h_, address, value)); }
@@ -555,6 +593,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("last_done_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_DONES); })
         .def("actions_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_ACTIONS); })
         .def("reset_envs", &CudaBatch::reset_envs, py::arg("mask"))
+        .def("reset_envs_device", &CudaBatch::reset_envs_device, py::arg("mask"))
         .def("poke_ram", &CudaBatch::poke_ram, py::arg("address"), py::arg("value"))
         .def("save_state", &CudaBatch::save_state, py::arg("env"))
         .def("load_state", &CudaBatch::load_state, py::arg("state"), py::arg("mask") = py::none())

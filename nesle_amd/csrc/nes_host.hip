@@ -534,7 +534,7 @@ int nesle_reset_envs(nesle_batch* b, const std::uint8_t* mask, int mask_on_devic
         }
         hip_check(nesle::launch_reset(b->ds, dmask, b->stream), "reset_kernel");
         b->refresh_obs();
-        b->sync();
+        if (!mask_on_device) b->sync();   // a device mask stays ordered on the stream
     });
 }
 

@@ -1,0 +1,438 @@
+"""GPU-resident PPO on the MI355X console: the drop-in for the reference's
+``nesle.native_ppo`` (src/nesle/native_ppo.py).
+
+Same configuration (``NativePPOConfig``), model (2,048 RAM bytes / 255 -> 256
+tanh -> 256 tanh -> action logits + value), GAE (``compute_gae``), clipped
+PPO loss, Adam, checkpoint fields and log line as the reference trainer
+(native_ppo.py:388-603).  The rollout keeps everything on the device and on
+one stream:
+
+* the batch runs on PyTorch's current stream (``CudaBatch.set_stream``), so
+  policy kernels, the step kernel and the RAM transpose are ordered without
+  host synchronisation;
+* done consoles are restored by the step kernel's fused auto-reset (the
+  reference calls ``reset_envs`` with a host mask after a ``done.any()`` host
+  read every step, native_ppo.py:498-507); the RAM view after the step shows
+  the post-reset state for them, exactly what the reference's
+  ``reset_envs`` + ``ram_device`` sequence returns;
+* episode-length timeouts (``max_episode_steps``) reset through a device
+  mask; episode returns are summed on the device and read once per log line;
+* the RAM, reward and done views are imported through DLPack once, before the
+  loop (their device buffers never move).
+
+``train_native_ppo`` returns the timing split the workload reports: wall time
+of rollout and update phases and the step kernel's own time (HIP events on
+the batch's stream), whose share of the wall time is the emulator share.
+"""
+
+from __future__ import annotations
+
+import argparse
+import math
+import time
+from dataclasses import asdict, dataclass, field
+from pathlib import Path
+from typing import Sequence
+
+import numpy as np
+
+from nesle_amd import actions as _actions
+
+
+@dataclass
+class NativePPOConfig:
+    rom_path: str
+    num_envs: int = 1024
+    total_timesteps: int = 1_000_000
+    n_steps: int = 128
+    batch_size: int = 8192
+    update_epochs: int = 4
+    frameskip: int = 4
+    action_space: str = "simple_with_start"
+    reset_state_path: str | None = None
+    reset_state_paths: tuple[str, ...] = ()
+    max_episode_steps: int = 0
+    learning_rate: float = 2.5e-4
+    gamma: float = 0.99
+    gae_lambda: float = 0.95
+    clip_coef: float = 0.1
+    ent_coef: float = 0.01
+    vf_coef: float = 0.5
+    max_grad_norm: float = 0.5
+    hidden_size: int = 256
+    reward_mode: str = "minimal"
+    seed: int = 1
+    checkpoint_path: str = "nesle_native_ppo.pt"
+    log_interval: int = 1
+    progress_bar: bool = False
+    # Additions: weight init ("orthogonal" as the reference trainer, or
+    # "xavier"), the in-kernel reward rule (CudaBatch ``reward=`` spec; None =
+    # the SMB rule), and whether to write checkpoints.
+    init: str = "orthogonal"
+    reward: dict | None = None
+    save_checkpoints: bool = True
+    env_to_level: tuple[int, ...] | None = field(default=None, repr=False)
+
+
+def _require_torch():
+    try:
+        import torch
+        import torch.nn as nn
+        from torch.distributions.categorical import Categorical
+    except ImportError as exc:  # pragma: no cover - torch is part of the image
+        raise SystemExit("native PPO needs PyTorch (ROCm build)") from exc
+    return torch, nn, Categorical
+
+
+def _make_model(obs_dim: int, action_dim: int, hidden_size: int, init: str = "orthogonal", device=None):
+    """The reference's RamActorCritic (native_ppo.py:76-101)."""
+    torch, nn, _ = _require_torch()
+    if init not in ("orthogonal", "xavier"):
+        raise ValueError(f"unknown init {init!r}: 'orthogonal' or 'xavier'")
+
+    def init_layer(layer, gain: float) -> None:
+        if init == "orthogonal":
+            nn.init.orthogonal_(layer.weight, gain)
+        else:
+            nn.init.xavier_uniform_(layer.weight, gain)
+        nn.init.constant_(layer.bias, 0.0)
+
+    class RamActorCritic(nn.Module):
+        def __init__(self) -> None:
+            super().__init__()
+            self.net = nn.Sequential(nn.Linear(obs_dim, hidden_size), nn.Tanh(),
+                                     nn.Linear(hidden_size, hidden_size), nn.Tanh())
+            self.actor = nn.Linear(hidden_size, action_dim)
+            self.critic = nn.Linear(hidden_size, 1)
+            for layer in self.net:
+                if isinstance(layer, nn.Linear):
+                    init_layer(layer, math.sqrt(2.0))
+            init_layer(self.actor, 0.01)
+            init_layer(self.critic, 1.0)
+
+        def forward(self, obs):
+            x = obs.float().div_(255.0)
+            features = self.net(x)
+            return self.actor(features), self.critic(features).squeeze(-1)
+
+    return RamActorCritic().to(device if device is not None else torch.device("cuda"))
+
+
+def compute_gae(rewards, dones, values, next_done, next_value, gamma: float, gae_lambda: float):
+    """Generalised advantage estimation over [T, N] tensors (native_ppo.py:609-624):
+    ``dones[t]`` marks that the observation at t started a new episode."""
+    torch, _, _ = _require_torch()
+    T = rewards.shape[0]
+    advantages = torch.empty_like(rewards)
+    lastgaelam = torch.zeros_like(rewards[0])
+    for t in range(T - 1, -1, -1):
+        if t == T - 1:
+            nonterminal, next_values = 1.0 - next_done, next_value
+        else:
+            nonterminal, next_values = 1.0 - dones[t + 1], values[t + 1]
+        delta = rewards[t] + gamma * next_values * nonterminal - values[t]
+        lastgaelam = delta + gamma * gae_lambda * nonterminal * lastgaelam
+        advantages[t] = lastgaelam
+    return advantages, advantages + values
+
+
+def _explained_variance(values, returns) -> float:
+    torch, _, _ = _require_torch()
+    with torch.no_grad():
+        y_var = torch.var(returns)
+        if float(y_var.item()) == 0.0:
+            return float("nan")
+        return float((1.0 - torch.var(returns - values) / y_var).item())
+
+
+# ---- checkpoints -----------------------------------------------------------
+# The reference stores numpy's RNG state as a pickled tuple and loads with
+# weights_only=False (native_ppo.py:324-368).  Here every field is a tensor,
+# number, string or list, so torch.load(weights_only=True) reads it back.
+
+def _save_checkpoint(path: str, model, optimizer, config: NativePPOConfig, global_step: int) -> None:
+    torch, _, _ = _require_torch()
+    name, keys, pos, has_gauss, cached = np.random.get_state()
+    cfg = {k: (list(v) if isinstance(v, tuple) else v) for k, v in asdict(config).items()}
+    payload = {
+        "model": model.state_dict(),
+        "optimizer": optimizer.state_dict(),
+        "config": cfg,
+        "global_step": int(global_step),
+        "torch_rng_state": torch.get_rng_state(),
+        "numpy_rng_state": [str(name), torch.from_numpy(np.asarray(keys, dtype=np.int64)), int(pos),
+                            int(has_gauss), float(cached)],
+    }
+    if torch.cuda.is_available():
+        payload["cuda_rng_state"] = torch.cuda.get_rng_state()
+    Path(path).resolve().parent.mkdir(parents=True, exist_ok=True)
+    torch.save(payload, path)
+
+
+def _load_checkpoint(path: str | None, model, optimizer) -> int:
+    if path is None or not Path(path).exists():
+        return 0
+    torch, _, _ = _require_torch()
+    map_location = "cuda" if torch.cuda.is_available() else "cpu"
+    payload = torch.load(path, map_location=map_location, weights_only=True)
+    model.load_state_dict(payload["model"])
+    optimizer.load_state_dict(payload["optimizer"])
+    if "torch_rng_state" in payload:
+        torch.set_rng_state(payload["torch_rng_state"].cpu())
+    if "cuda_rng_state" in payload and torch.cuda.is_available():
+        torch.cuda.set_rng_state(payload["cuda_rng_state"].cpu())
+    if "numpy_rng_state" in payload:
+        name, keys, pos, has_gauss, cached = payload["numpy_rng_state"]
+        np.random.set_state((name, keys.cpu().numpy().astype(np.uint32), pos, has_gauss, cached))
+    return int(payload.get("global_step", 0))
+
+
+# ---- environment -------------------------------------------------------------
+
+def make_batch(config: NativePPOConfig, rom_bytes: bytes | None = None,
+               snapshot_bytes: Sequence[bytes] | None = None):
+    """The HIP batch for a config: ROM from ``rom_path`` (or ``rom_bytes``), the
+    snapshot bank from ``reset_state_path(s)`` (or ``snapshot_bytes``; FCEUX FCS
+    or canonical blobs), levels round-robin unless ``env_to_level`` is given
+    (src/nesle/env.py:405-425), no frames (the policy reads RAM)."""
+    from nesle_amd import load_cuda_core
+
+    core = load_cuda_core()
+    rom = rom_bytes if rom_bytes is not None else Path(config.rom_path).read_bytes()
+    if snapshot_bytes is None:
+        if config.reset_state_path and config.reset_state_paths:
+            raise ValueError("pass either reset_state_path or reset_state_paths, not both")
+        paths = list(config.reset_state_paths) or ([config.reset_state_path] if config.reset_state_path else [])
+        snapshot_bytes = [Path(p).read_bytes() for p in paths]
+    kw = {"frames": False}
+    if config.reward is not None:
+        kw["reward"] = dict(config.reward)
+    n = config.num_envs
+    if not snapshot_bytes:
+        return core.CudaBatch(n, config.frameskip, rom, **kw)
+    if len(snapshot_bytes) == 1 and config.env_to_level is None:
+        return core.CudaBatch(n, config.frameskip, rom, bytes(snapshot_bytes[0]), **kw)
+    levels = (np.asarray(config.env_to_level, dtype=np.uint8) if config.env_to_level is not None
+              else (np.arange(n) % len(snapshot_bytes)).astype(np.uint8))
+    return core.CudaBatch(n, config.frameskip, rom, [bytes(s) for s in snapshot_bytes], levels, **kw)
+
+
+# ---- training ------------------------------------------------------------------
+
+def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *, rom_bytes: bytes | None = None,
+                     snapshot_bytes: Sequence[bytes] | None = None, batch=None, record=None) -> dict:
+    """Train; returns {"global_step", "updates", "rollout_s", "update_s",
+    "emulator_s", "wall_s", "log", "per_update", "model"} (emulator_s: step
+    kernel time from HIP events on the batch's stream).  ``record(step, actions, rewards, dones)``,
+    when given, receives each rollout step's device tensors (tests)."""
+    rollout_timesteps = config.num_envs * config.n_steps
+    if rollout_timesteps < config.batch_size:
+        raise ValueError(
+            f"rollout produces {rollout_timesteps} samples per update (num_envs={config.num_envs} * "
+            f"n_steps={config.n_steps}) but batch_size={config.batch_size} is larger")
+    if config.reward_mode != "minimal":
+        raise ValueError(f"reward_mode {config.reward_mode!r} is not provided: only 'minimal' "
+                         "(the batch's in-kernel reward rule)")
+    torch, _, Categorical = _require_torch()
+    if not torch.cuda.is_available():
+        raise SystemExit("native PPO needs a GPU")
+    torch.manual_seed(config.seed)
+    np.random.seed(config.seed)
+
+    masks = _actions.action_masks(config.action_space)
+    if batch is None:
+        batch = make_batch(config, rom_bytes, snapshot_bytes)
+    if batch.num_envs != config.num_envs or batch.frameskip != config.frameskip:
+        raise ValueError("batch shape does not match the config")
+    stream = torch.cuda.current_stream()
+    batch.set_stream(stream.cuda_stream)
+    batch.reset_device()
+
+    dev = torch.device("cuda")
+    obs_dim, action_dim, n = 2048, len(masks), config.num_envs
+    model = _make_model(obs_dim, action_dim, config.hidden_size, config.init, dev)
+    optimizer = torch.optim.Adam(model.parameters(), lr=config.learning_rate, eps=1e-5)
+    global_step = _load_checkpoint(resume_from, model, optimizer)
+    resume_step = global_step
+    mask_table = torch.tensor(masks, dtype=torch.uint8, device=dev)
+
+    from torch.utils.dlpack import from_dlpack
+
+    ram = from_dlpack(batch.ram_device())          # [N, 2048] uint8, refreshed by every step
+    rewards_view = from_dlpack(batch.rewards_device())
+    dones_view = from_dlpack(batch.last_done_device())
+
+    T = config.n_steps
+    obs_buf = torch.empty((T, n, obs_dim), dtype=torch.uint8, device=dev)
+    actions_buf = torch.empty((T, n), dtype=torch.long, device=dev)
+    logprobs_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
+    rewards_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
+    dones_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
+    values_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
+    episode_returns = torch.zeros(n, dtype=torch.float32, device=dev)
+    episode_lengths = torch.zeros(n, dtype=torch.float32, device=dev)
+    finished = torch.zeros(3, dtype=torch.float64, device=dev)   # episodes, return sum, length sum
+    next_done = torch.zeros(n, dtype=torch.float32, device=dev)
+
+    remaining = max(0, config.total_timesteps - global_step)
+    num_updates = math.ceil(remaining / rollout_timesteps)
+    stats = {"global_step": global_step, "updates": 0, "rollout_s": 0.0, "update_s": 0.0, "emulator_s": 0.0,
+             "wall_s": 0.0, "log": [], "per_update": []}
+    batch.set_timing(True)
+    t_start = time.perf_counter()
+    for update in range(1, num_updates + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for step in range(T):
+            global_step += n
+            obs_buf[step].copy_(ram)
+            dones_buf[step].copy_(next_done)
+            with torch.no_grad():
+                logits, value = model(ram)
+                dist = Categorical(logits=logits)
+                action = dist.sample()
+                logprobs_buf[step] = dist.log_prob(action)
+            actions_buf[step] = action
+            values_buf[step] = value
+            batch.step_device(mask_table[action], auto_reset=True, synchronize=False)
+            reward = rewards_view
+            done = dones_view.bool()
+            episode_lengths += 1.0
+            if config.max_episode_steps > 0:
+                timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
+                batch.reset_envs_device(timeout.to(torch.uint8))   # no-op for an all-zero mask
+                done = done | timeout
+            rewards_buf[step].copy_(reward)
+            next_done = done.float()
+            episode_returns += reward
+            finished[0] += next_done.sum()
+            finished[1] += (episode_returns * next_done).sum()
+            finished[2] += (episode_lengths * next_done).sum()
+            keep = 1.0 - next_done
+            episode_returns *= keep
+            episode_lengths *= keep
+            if record is not None:
+                record(step, mask_table[action], reward, done)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+
+        with torch.no_grad():
+            _, next_value = model(ram)
+            advantages, returns = compute_gae(rewards_buf, dones_buf, values_buf, next_done, next_value,
+                                              config.gamma, config.gae_lambda)
+        b_obs = obs_buf.reshape((-1, obs_dim))
+        b_actions = actions_buf.reshape(-1)
+        b_logprobs = logprobs_buf.reshape(-1)
+        b_advantages = advantages.reshape(-1)
+        b_returns = returns.reshape(-1)
+        b_values = values_buf.reshape(-1)
+        count = b_obs.shape[0]
+        clipfracs, losses = [], []
+        for _ in range(config.update_epochs):
+            perm = torch.randperm(count, device=dev)
+            for start in range(0, count, config.batch_size):
+                mb = perm[start:start + config.batch_size]
+                logits, newvalue = model(b_obs[mb])
+                dist = Categorical(logits=logits)
+                newlogprob = dist.log_prob(b_actions[mb])
+                entropy = dist.entropy().mean()
+                ratio = (newlogprob - b_logprobs[mb]).exp()
+                adv = b_advantages[mb]
+                adv = (adv - adv.mean()) / (adv.std() + 1e-8)
+                pg_loss = torch.max(-adv * ratio,
+                                    -adv * torch.clamp(ratio, 1.0 - config.clip_coef, 1.0 + config.clip_coef)).mean()
+                value_loss = 0.5 * (newvalue - b_returns[mb]).pow(2).mean()
+                loss = pg_loss - config.ent_coef * entropy + config.vf_coef * value_loss
+                optimizer.zero_grad(set_to_none=True)
+                loss.backward()
+                torch.nn.utils.clip_grad_norm_(model.parameters(), config.max_grad_norm)
+                optimizer.step()
+                with torch.no_grad():
+                    clipfracs.append(((ratio - 1.0).abs() > config.clip_coef).float().mean())
+                    losses.append(loss.detach())
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        stats["rollout_s"] += t1 - t0
+        stats["update_s"] += t2 - t1
+        stats["updates"] = update
+        kernel_ms, _ = batch.kernel_timing()
+        stats["per_update"].append({"rollout_s": t1 - t0, "update_s": t2 - t1,
+                                    "emulator_s": kernel_ms / 1000.0 - stats["emulator_s"]})
+        stats["emulator_s"] = kernel_ms / 1000.0
+
+        if update % max(1, config.log_interval) == 0 or update == num_updates:
+            fin = finished.tolist()
+            elapsed = max(1e-6, time.perf_counter() - t_start)
+            line = {
+                "update": update, "step": global_step, "fps": int((global_step - resume_step) / elapsed),
+                "loss": float(torch.stack(losses).mean()), "clipfrac": float(torch.stack(clipfracs).mean()),
+                "explained_var": _explained_variance(b_values, b_returns),
+                "episodes": int(fin[0]),
+                "ep_return_mean": fin[1] / fin[0] if fin[0] else float("nan"),
+                "ep_len_mean": fin[2] / fin[0] if fin[0] else float("nan"),
+            }
+            stats["log"].append(line)
+            print(f"update={update}/{num_updates} step={global_step} fps={line['fps']} loss={line['loss']:.4f} "
+                  f"clipfrac={line['clipfrac']:.3f} explained_var={line['explained_var']:.3f} "
+                  f"episodes={line['episodes']} ep_return={line['ep_return_mean']:.2f}", flush=True)
+            if config.save_checkpoints:
+                _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
+    torch.cuda.synchronize()
+    stats["wall_s"] = time.perf_counter() - t_start
+    batch.set_timing(False)
+    stats["global_step"] = global_step
+    if config.save_checkpoints and num_updates > 0:
+        _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
+    stats["model"] = model
+    return stats
+
+
+def parse_args() -> tuple[NativePPOConfig, str | None]:
+    p = argparse.ArgumentParser(description="Train with the GPU-resident PPO path on the MI355X console.")
+    p.add_argument("rom_path")
+    p.add_argument("--num-envs", type=int, default=1024)
+    p.add_argument("--total-timesteps", type=int, default=1_000_000)
+    p.add_argument("--n-steps", type=int, default=128)
+    p.add_argument("--batch-size", type=int, default=8192)
+    p.add_argument("--update-epochs", type=int, default=4)
+    p.add_argument("--frameskip", type=int, default=4)
+    p.add_argument("--action-space", default="simple_with_start",
+                   choices=["right_only", "simple", "simple_with_start", "complex", "mario", "raw"])
+    p.add_argument("--reset-state-path", default=None)
+    p.add_argument("--reset-state-paths", nargs="+", default=())
+    p.add_argument("--max-episode-steps", type=int, default=0)
+    p.add_argument("--learning-rate", type=float, default=2.5e-4)
+    p.add_argument("--gamma", type=float, default=0.99)
+    p.add_argument("--gae-lambda", type=float, default=0.95)
+    p.add_argument("--clip-coef", type=float, default=0.1)
+    p.add_argument("--ent-coef", type=float, default=0.01)
+    p.add_argument("--vf-coef", type=float, default=0.5)
+    p.add_argument("--max-grad-norm", type=float, default=0.5)
+    p.add_argument("--hidden-size", type=int, default=256)
+    p.add_argument("--reward-mode", default="minimal", choices=["minimal"])
+    p.add_argument("--init", default="orthogonal", choices=["orthogonal", "xavier"])
+    p.add_argument("--seed", type=int, default=1)
+    p.add_argument("--checkpoint-path", default="nesle_native_ppo.pt")
+    p.add_argument("--resume-from", default=None)
+    p.add_argument("--log-interval", type=int, default=1)
+    a = p.parse_args()
+    if a.reset_state_path and a.reset_state_paths:
+        raise SystemExit("Pass either --reset-state-path or --reset-state-paths, not both.")
+    cfg = NativePPOConfig(
+        rom_path=a.rom_path, num_envs=a.num_envs, total_timesteps=a.total_timesteps, n_steps=a.n_steps,
+        batch_size=a.batch_size, update_epochs=a.update_epochs, frameskip=a.frameskip, action_space=a.action_space,
+        reset_state_path=a.reset_state_path, reset_state_paths=tuple(a.reset_state_paths),
+        max_episode_steps=a.max_episode_steps, learning_rate=a.learning_rate, gamma=a.gamma,
+        gae_lambda=a.gae_lambda, clip_coef=a.clip_coef, ent_coef=a.ent_coef, vf_coef=a.vf_coef,
+        max_grad_norm=a.max_grad_norm, hidden_size=a.hidden_size, reward_mode=a.reward_mode, init=a.init,
+        seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval)
+    return cfg, a.resume_from
+
+
+def main() -> None:
+    cfg, resume = parse_args()
+    train_native_ppo(cfg, resume_from=resume)
+
+
+if __name__ == "__main__":
+    main()

@@ -7,7 +7,7 @@ import sys
 
 import numpy as np
 
-from nesle_amd import synthrom
+from nesle_amd import abi, synthrom
 from oracle import oracle as O
 
 
@@ -61,3 +61,19 @@ class OracleBatch:
 
 def masks_for(seed: int, num_envs: int, step: int) -> np.ndarray:
     return synthrom.action_masks(seed, num_envs, step)
+
+
+def warm_snapshots(rom: bytes, warm_frames: list[int], seed: int) -> list[np.ndarray]:
+    """Capture one snapshot per entry after that many frame-skip-1 frames."""
+    n = len(warm_frames)
+    b = abi.Batch(rom, n, frameskip=1)
+    for f in range(max(warm_frames) + 1):
+        for slot, wf in enumerate(warm_frames):
+            if wf == f:
+                b.snapshot_capture(slot, slot)
+        if f == max(warm_frames):
+            break
+        b.set_actions(masks_for(seed, n, f))
+        b.step()
+    assert b.num_levels == n
+    return [b.snapshot_export(s) for s in range(n)]

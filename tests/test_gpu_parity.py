@@ -17,7 +17,7 @@ import pytest
 
 from nesle_amd import abi, synthrom
 from oracle import oracle as O
-from tests.helpers import OracleBatch, first_diff, masks_for, say
+from tests.helpers import OracleBatch, first_diff, masks_for, say, warm_snapshots
 
 pytestmark = pytest.mark.gpu
 
@@ -110,22 +110,6 @@ def test_full_size_sampled_envs(num_envs, steps):
     assert (b.host(abi.VIEW_BUDGET_HITS) == 0).all()
 
 
-def _warm_snapshots(rom: bytes, warm_frames: list[int], seed: int) -> list[np.ndarray]:
-    """Capture one snapshot per entry after that many frame-skip-1 frames."""
-    n = len(warm_frames)
-    b = abi.Batch(rom, n, frameskip=1)
-    for f in range(max(warm_frames) + 1):
-        for slot, wf in enumerate(warm_frames):
-            if wf == f:
-                b.snapshot_capture(slot, slot)
-        if f == max(warm_frames):
-            break
-        b.set_actions(masks_for(seed, n, f))
-        b.step()
-    assert b.num_levels == n
-    return [b.snapshot_export(s) for s in range(n)]
-
-
 def test_snapshot_autoreset_xdelta_reward():
     """Config 3 in miniature: 8 snapshots captured after seeded warm-up frames,
     done byte patched so episodes end within the run, x-delta reward with time
@@ -135,7 +119,7 @@ def test_snapshot_autoreset_xdelta_reward():
     rom = rom_info.rom
     warm = [100, 150, 200, 250, 300, 350, 400, 450]
     say("[gpu] snapshot bank: warm-up capture of 8 levels")
-    snaps = _warm_snapshots(rom, warm, seed=55)
+    snaps = warm_snapshots(rom, warm, seed=55)
     for i, s in enumerate(snaps):
         s[O.OFF["ram"] + synthrom.DONE_BYTE] = 1 + i  # done after 8*(1+i) frames at most
     blobs = [bytes(s) for s in snaps]
