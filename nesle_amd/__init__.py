@@ -4,7 +4,11 @@
   (``CudaBatch``, ``CudaDeviceArrayView``, ``parse_fcs_state``), built by
   ``python -m nesle_amd.build`` over libnesle_hip.so;
 * ``nesle_amd.abi``         ctypes binding of the C ABI (include/nesle_hip.h);
-* ``nesle_amd.synthrom``    seeded synthetic NROM ROMs and controller streams.
+* ``nesle_amd.synthrom``    seeded synthetic NROM ROMs and controller streams;
+* ``nesle_amd.env``         SB3/Gymnasium vector and single environments
+  (``make_vec``, ``NesleVecEnv``, ``NesleEnv``), drop-in for ``nesle.env``;
+* ``nesle_amd.native_ppo``  GPU-resident PPO, drop-in for ``nesle.native_ppo``;
+* ``nesle_amd.actions``     controller masks and action sets.
 
 The native pieces are imported on first use, so importing the package never
 touches a GPU; using them without the built libraries raises ImportError.
@@ -12,7 +16,7 @@ touches a GPU; using them without the built libraries raises ImportError.
 
 from __future__ import annotations
 
-__all__ = ["load_cuda_core", "synthrom", "abi"]
+__all__ = ["load_cuda_core", "make_vec", "synthrom", "abi"]
 
 from . import abi, synthrom  # noqa: F401
 
@@ -22,3 +26,10 @@ def load_cuda_core():
     from . import _cuda_core  # type: ignore[attr-defined]
 
     return _cuda_core
+
+
+def make_vec(*args, **kwargs):
+    """``NesleVecEnv(*args, **kwargs)`` (the reference's ``nesle.make_vec``)."""
+    from .env import NesleVecEnv
+
+    return NesleVecEnv(*args, **kwargs)

@@ -1,0 +1,53 @@
+"""Host-side checks of the vector environment (no GPU): argument validation
+happens before any device work, observation-mode names, spaces without
+gymnasium, and reset-state file handling."""
+
+from __future__ import annotations
+
+import gzip
+
+import numpy as np
+import pytest
+
+from nesle_amd import env as E
+
+
+@pytest.mark.parametrize("kwargs", [dict(num_envs=0), dict(num_envs=2, frameskip=0),
+                                    dict(num_envs=2, observation_cadence=0), dict(num_envs=2, render_mode="human"),
+                                    dict(num_envs=2, backend="synthetic"), dict(num_envs=2, observation_mode="depth"),
+                                    dict(num_envs=2, action_space="sideways"),
+                                    dict(num_envs=2, reset_state_path="a", reset_state_paths=["b"])])
+def test_bad_arguments_are_rejected_before_device_work(kwargs):
+    with pytest.raises(ValueError):
+        E.NesleVecEnv("missing.nes", **kwargs)
+
+
+def test_env_to_level_checks(tmp_path):
+    a, b = tmp_path / "a.state", tmp_path / "b.state"
+    a.write_bytes(b"x")
+    b.write_bytes(b"y")
+    with pytest.raises(ValueError, match="requires more than one"):
+        E.NesleVecEnv("missing.nes", 2, reset_state_path=str(a), env_to_level=[0, 0])
+    with pytest.raises(ValueError, match="shape"):
+        E.NesleVecEnv("missing.nes", 2, reset_state_paths=[str(a), str(b)], env_to_level=[0])
+    with pytest.raises(ValueError, match=">= number"):
+        E.NesleVecEnv("missing.nes", 2, reset_state_paths=[str(a), str(b)], env_to_level=[0, 2])
+
+
+def test_observation_modes_and_spaces():
+    assert E._normalize_observation_mode("RGB") == "rgb_array"
+    assert E._normalize_observation_mode("cpu-ram") == "ram"
+    d = E.DiscreteSpace(12)
+    assert d.contains(11) and not d.contains(12) and not d.contains("x")
+    box = E.BoxSpace(0, 255, (2048,), np.uint8)
+    assert box.contains(box.sample())
+
+
+def test_gzip_reset_states_are_unpacked(tmp_path):
+    raw = bytes(range(256)) * 4
+    p = tmp_path / "level.state"
+    p.write_bytes(gzip.compress(raw))
+    assert E._load_reset_state(p) == raw
+    q = tmp_path / "plain.fcs"
+    q.write_bytes(raw)
+    assert E._load_reset_state(q) == raw
