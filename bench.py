@@ -13,7 +13,9 @@ of every console's 84x84 gray observation into device memory (100 steps by
 default; the full 2,000 take ``--pixel-steps 2000``), and the GPU-resident PPO
 workload: 8,192 consoles x 128 steps per update on the snapshot/x-delta setup,
 RAM MLP policy (12-way action space, Xavier init), GAE and 4 epochs of
-minibatch 8,192, with the step kernel's share of the update's wall time.
+minibatch 8,192, with the step kernel's share of the update's wall time; and
+the SB3/NumPy host path (``nesle_amd.env.NesleVecEnv`` at 4,096 consoles,
+RAM observations copied to host every step).
 
 Timed region: W untimed warm-up steps, synchronize, K timed steps of the
 Python-level ``CudaBatch.step_device(actions[k], auto_reset=True)`` loop (the
@@ -153,6 +155,28 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
     }
 
 
+def run_vec_env(rom: bytes, steps: int) -> dict:
+    """The SB3/NumPy host path: NesleVecEnv.step with host action indices,
+    RAM observations, rewards and dones copied to host NumPy every step,
+    auto-reset with terminal observations (12-way action space, episodes cut
+    at 500 steps)."""
+    from nesle_amd.env import NesleVecEnv
+
+    n = 4096
+    env = NesleVecEnv("synthetic.nes", n, frameskip=4, action_space="complex", observation_mode="ram",
+                      max_episode_steps=500, rom_bytes=rom)
+    env.reset()
+    acts = np.random.default_rng(ACTION_SEED).integers(0, 12, (steps + 5, n))
+    for k in range(5):
+        env.step(acts[k])
+    t0 = time.perf_counter()
+    for k in range(5, steps + 5):
+        env.step(acts[k])
+    dt = time.perf_counter() - t0
+    return {"num_envs": n, "steps": steps, "seconds": dt, "env_steps_per_s": n * steps / dt,
+            "ms_per_step": 1000.0 * dt / steps}
+
+
 def run_ppo(rom: bytes, snapshots: list[bytes], updates: int) -> dict:
     """GPU-resident PPO on the snapshot/x-delta setup: 8,192 consoles x 128
     steps per update, MLP on RAM, 12-way action space, Xavier init, GAE
@@ -247,6 +271,8 @@ def main() -> int:
     ap.add_argument("--small-steps", type=int, default=200)
     ap.add_argument("--pixel-envs", type=int, default=16384)
     ap.add_argument("--pixel-steps", type=int, default=100)
+    ap.add_argument("--vec-steps", type=int, default=50,
+                    help="steps of the SB3/NumPy vector env (4,096 consoles, RAM observations on the host; 0 skips)")
     ap.add_argument("--ppo-updates", type=int, default=2,
                     help="PPO updates of 8,192 consoles x 128 steps (the first warms up; 0 skips)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -281,6 +307,11 @@ def main() -> int:
     log(f"timing {args.small_envs} envs x {args.small_steps} steps (no resets)")
     small = run_gpu(core, rom, args.small_envs, args.small_steps, max(5, args.warmup // 4), None, None)
     log(f"  {small['env_steps_per_s']:.0f} env-steps/s")
+    vec = None
+    if args.vec_steps > 0:
+        log(f"SB3 vector env: 4096 envs x {args.vec_steps} steps, RAM observations to host")
+        vec = run_vec_env(rom, args.vec_steps)
+        log(f"  {vec['env_steps_per_s']:.0f} env-steps/s")
     ppo = None
     if args.ppo_updates > 0:
         log(f"PPO: 8192 envs x 128 steps, {args.ppo_updates} updates")
@@ -336,7 +367,8 @@ def main() -> int:
             "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
         },
-        "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel, "ppo_8192x128": ppo},
+        "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel, "ppo_8192x128": ppo,
+                  "vec_env_ram_4096": vec},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
