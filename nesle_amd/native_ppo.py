@@ -67,10 +67,12 @@ class NativePPOConfig:
     progress_bar: bool = False
     # Additions: weight init ("orthogonal" as the reference trainer, or
     # "xavier"), the in-kernel reward rule (CudaBatch ``reward=`` spec; None =
-    # the SMB rule), and whether to write checkpoints.
+    # the SMB rule), whether to write checkpoints, and whether rollouts after
+    # the first replay a captured HIP graph.
     init: str = "orthogonal"
     reward: dict | None = None
     save_checkpoints: bool = True
+    cuda_graph: bool = True
     env_to_level: tuple[int, ...] | None = field(default=None, repr=False)
 
 
@@ -219,12 +221,41 @@ def make_batch(config: NativePPOConfig, rom_bytes: bytes | None = None,
 
 # ---- training ------------------------------------------------------------------
 
+def _capture_rollout(torch, batch, rollout_step, T: int, model, ram):
+    """Capture T rollout steps into one HIP graph.  The batch's kernels are
+    enqueued on the capture stream (its stream is switched for the capture
+    and switched back), the policy is warmed up on that stream first, and the
+    captured work holds no memset or host synchronisation: sampling noise is
+    drawn before each replay and the episode statistics are per-console sums."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.no_grad():
+        for _ in range(2):
+            model(ram)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    batch.set_stream(side.cuda_stream)
+    try:
+        with torch.cuda.graph(graph, stream=side):
+            for t in range(T):
+                rollout_step(t)
+    finally:
+        torch.cuda.synchronize()
+        batch.set_stream(torch.cuda.current_stream().cuda_stream)
+    return graph
+
+
 def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *, rom_bytes: bytes | None = None,
-                     snapshot_bytes: Sequence[bytes] | None = None, batch=None, record=None) -> dict:
+                     snapshot_bytes: Sequence[bytes] | None = None, batch=None, record=None,
+                     on_rollout=None) -> dict:
     """Train; returns {"global_step", "updates", "rollout_s", "update_s",
-    "emulator_s", "wall_s", "log", "per_update", "model"} (emulator_s: step
-    kernel time from HIP events on the batch's stream).  ``record(step, actions, rewards, dones)``,
-    when given, receives each rollout step's device tensors (tests)."""
+    "emulator_s", "wall_s", "log", "per_update", "graph_updates", "model"}
+    (emulator_s: step-kernel time per rollout step from HIP events on the
+    batch's stream during the eager first rollout, times the steps).
+    ``record(step, masks, rewards, dones)`` receives each step's device tensors
+    and keeps every rollout eager; ``on_rollout(update, buffers)`` receives
+    the rollout buffers after each rollout (tests)."""
     rollout_timesteps = config.num_envs * config.n_steps
     if rollout_timesteps < config.batch_size:
         raise ValueError(
@@ -271,50 +302,81 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     values_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
     episode_returns = torch.zeros(n, dtype=torch.float32, device=dev)
     episode_lengths = torch.zeros(n, dtype=torch.float32, device=dev)
-    finished = torch.zeros(3, dtype=torch.float64, device=dev)   # episodes, return sum, length sum
+    # Finished episodes per console (count, return sum, length sum), summed at log time.
+    fin_count = torch.zeros(n, dtype=torch.float32, device=dev)
+    fin_return = torch.zeros(n, dtype=torch.float64, device=dev)
+    fin_length = torch.zeros(n, dtype=torch.float64, device=dev)
     next_done = torch.zeros(n, dtype=torch.float32, device=dev)
+    noise = torch.empty((T, n, action_dim), dtype=torch.float32, device=dev)
+    rows = torch.arange(n, device=dev)
+
+    def rollout_step(t: int) -> None:
+        """One rollout step, entirely on the device: policy, sampling, the
+        console step and episode bookkeeping (captured into a graph as is)."""
+        obs_buf[t].copy_(ram)
+        dones_buf[t].copy_(next_done)
+        with torch.no_grad():
+            logits, value = model(ram)
+            # Categorical sample by Gumbel-max over uniforms drawn before the
+            # rollout (same distribution as Categorical.sample).
+            action = (logits - torch.log(-torch.log(noise[t]))).argmax(dim=-1)
+            logprobs_buf[t].copy_(torch.log_softmax(logits, dim=-1)[rows, action])
+        actions_buf[t].copy_(action)
+        values_buf[t].copy_(value)
+        batch.step_device(mask_table[action], auto_reset=True, synchronize=False)
+        done = dones_view.bool()
+        episode_lengths.add_(1.0)
+        if config.max_episode_steps > 0:
+            timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
+            batch.reset_envs_device(timeout.to(torch.uint8))   # consoles not in the mask are untouched
+            done = done | timeout
+        rewards_buf[t].copy_(rewards_view)
+        next_done.copy_(done.float())
+        episode_returns.add_(rewards_view)
+        fin_count.add_(next_done)
+        fin_return.add_(episode_returns * next_done)
+        fin_length.add_(episode_lengths * next_done)
+        keep = 1.0 - next_done
+        episode_returns.mul_(keep)
+        episode_lengths.mul_(keep)
 
     remaining = max(0, config.total_timesteps - global_step)
     num_updates = math.ceil(remaining / rollout_timesteps)
     stats = {"global_step": global_step, "updates": 0, "rollout_s": 0.0, "update_s": 0.0, "emulator_s": 0.0,
-             "wall_s": 0.0, "log": [], "per_update": []}
-    batch.set_timing(True)
+             "wall_s": 0.0, "log": [], "per_update": [], "graph_updates": 0}
+    graph = None
+    step_ms = None   # step-kernel time per rollout step, from the eager first rollout
     t_start = time.perf_counter()
     for update in range(1, num_updates + 1):
+        # The first rollout runs eagerly (HIP-event timing of the step kernel,
+        # library warm-up); with cuda_graph the later ones replay a graph of
+        # all T steps captured once.
+        use_graph = config.cuda_graph and update > 1 and record is None
+        if use_graph and graph is None:
+            graph = _capture_rollout(torch, batch, rollout_step, T, model, ram)
+        noise.uniform_(1e-20, 1.0)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for step in range(T):
-            global_step += n
-            obs_buf[step].copy_(ram)
-            dones_buf[step].copy_(next_done)
-            with torch.no_grad():
-                logits, value = model(ram)
-                dist = Categorical(logits=logits)
-                action = dist.sample()
-                logprobs_buf[step] = dist.log_prob(action)
-            actions_buf[step] = action
-            values_buf[step] = value
-            batch.step_device(mask_table[action], auto_reset=True, synchronize=False)
-            reward = rewards_view
-            done = dones_view.bool()
-            episode_lengths += 1.0
-            if config.max_episode_steps > 0:
-                timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
-                batch.reset_envs_device(timeout.to(torch.uint8))   # no-op for an all-zero mask
-                done = done | timeout
-            rewards_buf[step].copy_(reward)
-            next_done = done.float()
-            episode_returns += reward
-            finished[0] += next_done.sum()
-            finished[1] += (episode_returns * next_done).sum()
-            finished[2] += (episode_lengths * next_done).sum()
-            keep = 1.0 - next_done
-            episode_returns *= keep
-            episode_lengths *= keep
-            if record is not None:
-                record(step, mask_table[action], reward, done)
+        if use_graph:
+            graph.replay()
+        else:
+            batch.set_timing(True)
+            for t in range(T):
+                rollout_step(t)
+                if record is not None:
+                    record(t, mask_table[actions_buf[t]], rewards_buf[t], next_done.bool())
+        global_step += rollout_timesteps
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        if not use_graph:
+            kernel_ms, launches = batch.kernel_timing()
+            batch.set_timing(False)
+            step_ms = kernel_ms / max(launches, 1)
+        else:
+            stats["graph_updates"] += 1
+        if on_rollout is not None:
+            on_rollout(update, {"actions": actions_buf, "rewards": rewards_buf, "dones": dones_buf,
+                                "values": values_buf, "logprobs": logprobs_buf, "graph": use_graph})
 
         with torch.no_grad():
             _, next_value = model(ram)
@@ -355,13 +417,13 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         stats["rollout_s"] += t1 - t0
         stats["update_s"] += t2 - t1
         stats["updates"] = update
-        kernel_ms, _ = batch.kernel_timing()
-        stats["per_update"].append({"rollout_s": t1 - t0, "update_s": t2 - t1,
-                                    "emulator_s": kernel_ms / 1000.0 - stats["emulator_s"]})
-        stats["emulator_s"] = kernel_ms / 1000.0
+        emu = step_ms * T / 1000.0
+        stats["per_update"].append({"rollout_s": t1 - t0, "update_s": t2 - t1, "emulator_s": emu,
+                                    "graph": use_graph})
+        stats["emulator_s"] += emu
 
         if update % max(1, config.log_interval) == 0 or update == num_updates:
-            fin = finished.tolist()
+            fin = [float(fin_count.sum()), float(fin_return.sum()), float(fin_length.sum())]
             elapsed = max(1e-6, time.perf_counter() - t_start)
             line = {
                 "update": update, "step": global_step, "fps": int((global_step - resume_step) / elapsed),
@@ -379,7 +441,6 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     torch.cuda.synchronize()
     stats["wall_s"] = time.perf_counter() - t_start
-    batch.set_timing(False)
     stats["global_step"] = global_step
     if config.save_checkpoints and num_updates > 0:
         _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)

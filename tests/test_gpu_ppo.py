@@ -70,3 +70,37 @@ def test_ppo_rollout_matches_oracle_and_update_learns(max_episode_steps):
     init = P._make_model(2048, 12, 256, "xavier", torch.device("cuda"))
     moved = [not torch.equal(a, b) for a, b in zip(init.parameters(), stats["model"].parameters())]
     assert all(moved)
+
+
+def test_rollout_graph_replays_match_eager_rollouts():
+    """With cuda_graph the rollouts after the first replay one captured HIP
+    graph (policy, sampling, the C-ABI step and bookkeeping for all steps).
+    Every replay, with the eager update and host synchronisations between
+    replays, equals the same rollout run eagerly."""
+    rom = synthrom.make_rom(5).rom
+    snaps = warm_snapshots(rom, [100, 150, 200, 250], seed=55)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 2 + i
+    n, T, updates = 64, 8, 4
+    reward = dict(kind="x_delta", x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE,
+                  clip=15, time_penalty=0.25)
+    runs = {}
+    for graph in (False, True):
+        say(f"[gpu] ppo rollouts cuda_graph={graph}: N={n} T={T} updates={updates}")
+        cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, n_steps=T, batch_size=128, update_epochs=1,
+                                frameskip=4, action_space="complex", init="xavier", reward=reward,
+                                total_timesteps=n * T * updates, save_checkpoints=False, seed=11,
+                                max_episode_steps=6, cuda_graph=graph)
+        got = []
+        stats = P.train_native_ppo(cfg, rom_bytes=rom, snapshot_bytes=[bytes(s) for s in snaps],
+                                   on_rollout=lambda u, b: got.append(
+                                       {k: (v.cpu().numpy().copy() if hasattr(v, "cpu") else v) for k, v in b.items()}))
+        runs[graph] = got
+        assert stats["graph_updates"] == (updates - 1 if graph else 0)
+    assert [r["graph"] for r in runs[True]] == [False] + [True] * (updates - 1)
+    for u, (e, g) in enumerate(zip(runs[False], runs[True])):
+        for key in ("actions", "rewards", "dones"):
+            np.testing.assert_array_equal(g[key], e[key], err_msg=f"update {u + 1} {key}")
+        for key in ("values", "logprobs"):
+            np.testing.assert_allclose(g[key], e[key], rtol=0, atol=1e-5, err_msg=f"update {u + 1} {key}")
+    assert sum(int(r["dones"].sum()) for r in runs[True]) > 0
