@@ -1,0 +1,128 @@
+"""Step-kernel paths the synthetic benchmark ROM never takes, against the
+oracle: PRG RAM reads and writes, code executing from RAM (fetched through
+the bus), `JMP ($xxFF)` with the 6502 page-wrap, a stack driven 192 bytes
+deep (below the LDS-resident $0180-$01FF when RAM is split), OAM DMA from
+RAM, PRG RAM, PRG ROM and PPU register pages (`$2000-$20FF`: reads with
+their side effects), and illegal opcodes that stop a console.  Both LDS
+layouts run: all RAM in LDS (64 consoles) and split RAM (16,384 consoles,
+sampled)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from nesle_amd import abi
+from nesle_amd.synthrom import _Asm
+from oracle import oracle as O
+from tests.helpers import first_diff, masks_for, say
+
+pytestmark = pytest.mark.gpu
+
+
+def feature_rom() -> bytes:
+    a = _Asm()
+    a.org(0x8000)
+    a.op("SEI"); a.op("CLD"); a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("LDX", "imm", 6)                       # copy the RAM routine to $0300
+    cp = a.label()
+    a.op("LDA", "absx", 0x8100); a.op("STA", "absx", 0x0300); a.op("DEX"); a.op("BPL", "rel", cp)
+    a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x0400)   # vector $0400 -> $8200
+    a.op("LDA", "imm", 0x82); a.op("STA", "abs", 0x0401)
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)   # NMI on
+    a.op("LDA", "imm", 0x1E); a.op("STA", "abs", 0x2001)
+    a.op("JMP", "ind", 0x0400)
+    a.org(0x8100)                               # RAM routine: $12 = buttons ^ $5A
+    a.byte(0xA5, 0x10, 0x49, 0x5A, 0x85, 0x12, 0x60)
+    a.org(0x8200)
+    a.label("MAIN")
+    a.op("INC", "zp", 0x20); a.op("LDX", "zp", 0x20)
+    a.op("TXA"); a.op("STA", "absx", 0x6000)              # PRG RAM write
+    a.op("LDA", "absx", 0x7F00); a.op("STA", "zp", 0x21)  # PRG RAM read
+    a.op("LDA", "absx", 0x6000); a.op("CLC"); a.op("ADC", "zp", 0x21); a.op("STA", "absx", 0x6100)
+    a.op("JSR", "abs", 0x0300)                            # code in RAM
+    a.op("LDA", "zp", 0x10); a.op("AND", "imm", 0x01); a.op("BEQ", "rel", "nodeep")
+    a.op("LDX", "imm", 0xC0)
+    push = a.label()
+    a.op("PHA"); a.op("DEX"); a.op("BNE", "rel", push)
+    a.op("LDX", "imm", 0xC0)
+    pull = a.label()
+    a.op("PLA"); a.op("DEX"); a.op("BNE", "rel", pull)
+    a.label("nodeep")
+    a.op("LDA", "zp", 0x10); a.op("AND", "imm", 0x02); a.op("BEQ", "rel", "nowrap")
+    a.op("LDA", "imm", "back"); a.op("STA", "abs", 0x04FF)   # JMP ($04FF) takes its high byte
+    a.op("LDA", "imm", 0x82); a.op("STA", "abs", 0x0400)     # from $0400, not $0500
+    a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x0500)
+    a.op("JMP", "ind", 0x04FF)
+    a.byte(0x02)                                # reached only without the page wrap
+    a.label("back")
+    a.label("nowrap")
+    a.op("LDA", "zp", 0x10); a.op("AND", "imm", 0xF0); a.op("CMP", "imm", 0xF0); a.op("BNE", "rel", "noill")
+    a.byte(0x02)                                # illegal: the console stops
+    a.label("noill")
+    a.op("JMP", "abs", "MAIN")
+    a.org(0x9000)                               # NMI: read pad 1, OAM DMA from a rotating page
+    a.op("PHA"); a.op("TXA"); a.op("PHA")
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016); a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDX", "imm", 8)
+    rd = a.label()
+    a.op("LDA", "abs", 0x4016); a.op("LSR", "acc"); a.op("ROL", "zp", 0x10); a.op("DEX"); a.op("BNE", "rel", rd)
+    a.op("INC", "zp", 0x11)
+    a.op("LDA", "zp", 0x11); a.op("AND", "imm", 3); a.op("TAX"); a.op("LDA", "absx", 0x9100)
+    a.op("STA", "abs", 0x4014)
+    a.op("PLA"); a.op("TAX"); a.op("PLA"); a.op("RTI")
+    a.org(0x9100)
+    a.byte(0x02, 0x60, 0x80, 0x20)              # DMA pages: RAM, PRG RAM, PRG ROM, PPU registers
+    a.resolve()
+    prg = bytearray(a.prg)
+    for at, v in ((0xFFFA, 0x9000), (0xFFFC, 0x8000), (0xFFFE, 0x8000)):
+        prg[at - 0x8000] = v & 0xFF
+        prg[at - 0x8000 + 1] = v >> 8
+    chr_rom = bytes((i * 37 + 11) & 0xFF for i in range(0x2000))
+    return bytes(b"NES\x1a" + bytes([2, 1, 0x01, 0]) + bytes(8)) + bytes(prg) + chr_rom
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_rare_paths_match_oracle(num_envs):
+    rom = feature_rom()
+    steps = 12
+    sample = list(range(64)) if num_envs == 64 else sorted({0, 1, 63, 64, 4095, 8191, 12000, num_envs - 1,
+                                                             *np.random.default_rng(7).integers(0, num_envs, 8)})
+    say(f"[gpu] rare paths: N={num_envs} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    cons = {e: O.Oracle(rom) for e in sample}
+    for c in cons.values():
+        c.set_reward()
+    stopped: dict[int, int] = {}
+    deep = wrapped = 0
+    for k in range(steps):
+        m = masks_for(909, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, don = b.host(abi.VIEW_INSTRUCTIONS), b.host(abi.VIEW_REWARDS), b.host(abi.VIEW_DONES)
+        for e, c in cons.items():
+            if e in stopped:
+                assert don[e] == 1 and rew[e] == 0.0, f"stopped env {e}"
+                continue
+            try:
+                n, r, d = c.step(int(m[e]), 4)
+            except RuntimeError:
+                stopped[e] = k
+                assert don[e] == 1 and rew[e] == 0.0, f"env {e} stopped at step {k}"
+                continue
+            assert ins[e] == n and rew[e] == np.float32(r) and don[e] == d, f"step {k} env {e}"
+            deep += int(m[e] & 1)
+            wrapped += int((m[e] >> 1) & 1)
+        if k % 4 == 3 or k == steps - 1:
+            for e, c in cons.items():
+                got, ref = b.save_state(e), c.save()
+                if e in stopped:
+                    # The oracle's PC has moved past the illegal opcode; the
+                    # stopped console's pad latch still takes each step's
+                    # buttons.  Everything else is frozen.
+                    got, ref = got.copy(), ref.copy()
+                    for name, size in (("pc", 2), ("c1_buttons", 1), ("c1_shift", 1), ("c1_count", 1)):
+                        got[O.OFF[name]:O.OFF[name] + size] = ref[O.OFF[name]:O.OFF[name] + size]
+                    assert got[O.OFF["fault"]] & 1
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert stopped and len(stopped) < len(sample) and deep and wrapped
