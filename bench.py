@@ -1,6 +1,6 @@
 """Benchmark: env-steps/s (frame-skip 4) of the MI355X batched NROM console.
 
-Workload (the north-star configuration, one GPU): 65,536 consoles on the
+Workload (one GPU): 65,536 consoles on the
 seeded synthetic NROM ROM, RAM observation, frame-skip 4, each console on its
 own counter-based pad stream (one uniformly drawn mask per step, held for the
 step's 4 frames); done fires when the ROM's countdown byte reaches 0 and the
