@@ -246,6 +246,106 @@ def _capture_rollout(torch, batch, rollout_step, T: int, model, ram):
     return graph
 
 
+def _set_capturable(torch, optimizer, capturable: bool) -> None:
+    """Adam with its step counters on the device (``capturable``) runs inside
+    a captured graph; a checkpoint restores the flag it was saved with, so it
+    is set again after loading and the counters are moved to match."""
+    for group in optimizer.param_groups:
+        group["capturable"] = capturable
+        for p in group["params"]:
+            state = optimizer.state.get(p)
+            if state and "step" in state:
+                device = p.device if capturable else torch.device("cpu")
+                state["step"] = state["step"].to(dtype=torch.float32, device=device)
+
+
+class MinibatchUpdate:
+    """Clipped-PPO minibatch steps over the rollout buffers
+    (native_ppo.py:540-575): forward, loss, backward, gradient-norm clipping
+    and Adam, with the loss and clip fraction summed on the device.
+
+    ``run(idx)`` takes one minibatch of sample indices.  After ``capture()``
+    a full minibatch replays one HIP graph of the whole step instead (about
+    60 launches each): ``idx`` is copied into the graph's index buffer and
+    the graph gathers the minibatch from ``sources``, whose device buffers
+    must stay in place.  The captured work holds no host synchronisation
+    (the distribution skips argument validation, clipping is a device-side
+    scale, Adam is ``capturable``)."""
+
+    def __init__(self, torch, Categorical, model, optimizer, config: NativePPOConfig, sources: dict):
+        self.torch, self.Categorical = torch, Categorical
+        self.model, self.optimizer, self.config = model, optimizer, config
+        self.sources = sources          # obs, actions, logprobs, advantages, returns: [count, ...]
+        dev = sources["obs"].device
+        self.sums = torch.zeros(2, dtype=torch.float32, device=dev)    # loss, clip fraction
+        self.minibatches = 0
+        self.idx = torch.zeros(config.batch_size, dtype=torch.long, device=dev)
+        self.graph = None
+
+    def _loss(self, idx):
+        torch, cfg, src = self.torch, self.config, self.sources
+        logits, newvalue = self.model(src["obs"][idx])
+        dist = self.Categorical(logits=logits, validate_args=False)
+        newlogprob = dist.log_prob(src["actions"][idx])
+        entropy = dist.entropy().mean()
+        ratio = (newlogprob - src["logprobs"][idx]).exp()
+        adv = src["advantages"][idx]
+        adv = (adv - adv.mean()) / (adv.std() + 1e-8)
+        pg_loss = torch.max(-adv * ratio, -adv * torch.clamp(ratio, 1.0 - cfg.clip_coef, 1.0 + cfg.clip_coef)).mean()
+        value_loss = 0.5 * (newvalue - src["returns"][idx]).pow(2).mean()
+        return pg_loss - cfg.ent_coef * entropy + cfg.vf_coef * value_loss, ratio
+
+    def _step(self, idx) -> None:
+        torch = self.torch
+        loss, ratio = self._loss(idx)
+        self.optimizer.zero_grad(set_to_none=True)
+        loss.backward()
+        torch.nn.utils.clip_grad_norm_(self.model.parameters(), self.config.max_grad_norm)
+        self.optimizer.step()
+        with torch.no_grad():
+            clipfrac = ((ratio - 1.0).abs() > self.config.clip_coef).float().mean()
+            self.sums.add_(torch.stack([loss.detach(), clipfrac]))
+
+    def run(self, idx) -> None:
+        if self.graph is not None and idx.shape[0] == self.idx.shape[0]:
+            self.idx.copy_(idx)
+            self.graph.replay()
+        else:
+            self._step(idx)
+        self.minibatches += 1
+
+    def capture(self) -> None:
+        """Capture one full-minibatch step.  Forward and backward are warmed
+        up on the capture stream first (library handles and workspaces for
+        that stream; the warm-up's gradients are dropped, no parameter
+        changes), and the gradients are released so the captured backward
+        writes them afresh on every replay."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                loss, _ = self._loss(self.idx)
+                loss.backward()
+                self.optimizer.zero_grad(set_to_none=True)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            self._step(self.idx)
+        torch.cuda.synchronize()
+        self.graph = graph
+
+    def reset_sums(self) -> None:
+        self.sums.zero_()
+        self.minibatches = 0
+
+    def means(self) -> tuple[float, float]:
+        """(mean loss, mean clip fraction) over the minibatches since ``reset_sums``."""
+        loss, clipfrac = (self.sums / max(self.minibatches, 1)).tolist()
+        return loss, clipfrac
+
+
 def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *, rom_bytes: bytes | None = None,
                      snapshot_bytes: Sequence[bytes] | None = None, batch=None, record=None,
                      on_rollout=None) -> dict:
@@ -282,8 +382,12 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     dev = torch.device("cuda")
     obs_dim, action_dim, n = 2048, len(masks), config.num_envs
     model = _make_model(obs_dim, action_dim, config.hidden_size, config.init, dev)
-    optimizer = torch.optim.Adam(model.parameters(), lr=config.learning_rate, eps=1e-5)
+    # Adam keeps its step counters on the device in both modes (the captured
+    # minibatch step needs it), so eager and graph training compute the same
+    # numbers.
+    optimizer = torch.optim.Adam(model.parameters(), lr=config.learning_rate, eps=1e-5, capturable=True)
     global_step = _load_checkpoint(resume_from, model, optimizer)
+    _set_capturable(torch, optimizer, True)
     resume_step = global_step
     mask_table = torch.tensor(masks, dtype=torch.uint8, device=dev)
 
@@ -307,6 +411,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     fin_return = torch.zeros(n, dtype=torch.float64, device=dev)
     fin_length = torch.zeros(n, dtype=torch.float64, device=dev)
     next_done = torch.zeros(n, dtype=torch.float32, device=dev)
+    adv_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
+    ret_buf = torch.empty((T, n), dtype=torch.float32, device=dev)
     noise = torch.empty((T, n, action_dim), dtype=torch.float32, device=dev)
     rows = torch.arange(n, device=dev)
 
@@ -340,6 +446,11 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         episode_returns.mul_(keep)
         episode_lengths.mul_(keep)
 
+    updater = MinibatchUpdate(torch, Categorical, model, optimizer, config, {
+        "obs": obs_buf.reshape((-1, obs_dim)), "actions": actions_buf.reshape(-1),
+        "logprobs": logprobs_buf.reshape(-1), "advantages": adv_buf.reshape(-1), "returns": ret_buf.reshape(-1)})
+    update_graph_ok = config.cuda_graph and rollout_timesteps % config.batch_size == 0
+
     remaining = max(0, config.total_timesteps - global_step)
     num_updates = math.ceil(remaining / rollout_timesteps)
     stats = {"global_step": global_step, "updates": 0, "rollout_s": 0.0, "update_s": 0.0, "emulator_s": 0.0,
@@ -350,10 +461,12 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     for update in range(1, num_updates + 1):
         # The first rollout runs eagerly (HIP-event timing of the step kernel,
         # library warm-up); with cuda_graph the later ones replay a graph of
-        # all T steps captured once.
+        # all T steps captured once, and so do the minibatch steps.
         use_graph = config.cuda_graph and update > 1 and record is None
         if use_graph and graph is None:
             graph = _capture_rollout(torch, batch, rollout_step, T, model, ram)
+        if use_graph and update_graph_ok and updater.graph is None:
+            updater.capture()
         noise.uniform_(1e-20, 1.0)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -382,36 +495,17 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
             _, next_value = model(ram)
             advantages, returns = compute_gae(rewards_buf, dones_buf, values_buf, next_done, next_value,
                                               config.gamma, config.gae_lambda)
-        b_obs = obs_buf.reshape((-1, obs_dim))
-        b_actions = actions_buf.reshape(-1)
-        b_logprobs = logprobs_buf.reshape(-1)
-        b_advantages = advantages.reshape(-1)
-        b_returns = returns.reshape(-1)
-        b_values = values_buf.reshape(-1)
-        count = b_obs.shape[0]
-        clipfracs, losses = [], []
+            adv_buf.copy_(advantages)
+            ret_buf.copy_(returns)
+        # Minibatch updates: the first update runs eagerly; with cuda_graph
+        # and minibatches that tile the rollout, the later ones replay the
+        # captured graph of one minibatch step per minibatch.
+        count = rollout_timesteps
+        updater.reset_sums()
         for _ in range(config.update_epochs):
             perm = torch.randperm(count, device=dev)
             for start in range(0, count, config.batch_size):
-                mb = perm[start:start + config.batch_size]
-                logits, newvalue = model(b_obs[mb])
-                dist = Categorical(logits=logits)
-                newlogprob = dist.log_prob(b_actions[mb])
-                entropy = dist.entropy().mean()
-                ratio = (newlogprob - b_logprobs[mb]).exp()
-                adv = b_advantages[mb]
-                adv = (adv - adv.mean()) / (adv.std() + 1e-8)
-                pg_loss = torch.max(-adv * ratio,
-                                    -adv * torch.clamp(ratio, 1.0 - config.clip_coef, 1.0 + config.clip_coef)).mean()
-                value_loss = 0.5 * (newvalue - b_returns[mb]).pow(2).mean()
-                loss = pg_loss - config.ent_coef * entropy + config.vf_coef * value_loss
-                optimizer.zero_grad(set_to_none=True)
-                loss.backward()
-                torch.nn.utils.clip_grad_norm_(model.parameters(), config.max_grad_norm)
-                optimizer.step()
-                with torch.no_grad():
-                    clipfracs.append(((ratio - 1.0).abs() > config.clip_coef).float().mean())
-                    losses.append(loss.detach())
+                updater.run(perm[start:start + config.batch_size])
         torch.cuda.synchronize()
         t2 = time.perf_counter()
         stats["rollout_s"] += t1 - t0
@@ -419,16 +513,17 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         stats["updates"] = update
         emu = step_ms * T / 1000.0
         stats["per_update"].append({"rollout_s": t1 - t0, "update_s": t2 - t1, "emulator_s": emu,
-                                    "graph": use_graph})
+                                    "graph": use_graph, "update_graph": updater.graph is not None})
         stats["emulator_s"] += emu
 
         if update % max(1, config.log_interval) == 0 or update == num_updates:
             fin = [float(fin_count.sum()), float(fin_return.sum()), float(fin_length.sum())]
+            mean_loss, mean_clipfrac = updater.means()
             elapsed = max(1e-6, time.perf_counter() - t_start)
             line = {
                 "update": update, "step": global_step, "fps": int((global_step - resume_step) / elapsed),
-                "loss": float(torch.stack(losses).mean()), "clipfrac": float(torch.stack(clipfracs).mean()),
-                "explained_var": _explained_variance(b_values, b_returns),
+                "loss": mean_loss, "clipfrac": mean_clipfrac,
+                "explained_var": _explained_variance(values_buf.reshape(-1), ret_buf.reshape(-1)),
                 "episodes": int(fin[0]),
                 "ep_return_mean": fin[1] / fin[0] if fin[0] else float("nan"),
                 "ep_len_mean": fin[2] / fin[0] if fin[0] else float("nan"),

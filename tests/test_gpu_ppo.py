@@ -74,9 +74,10 @@ def test_ppo_rollout_matches_oracle_and_update_learns(max_episode_steps):
 
 def test_rollout_graph_replays_match_eager_rollouts():
     """With cuda_graph the rollouts after the first replay one captured HIP
-    graph (policy, sampling, the C-ABI step and bookkeeping for all steps).
-    Every replay, with the eager update and host synchronisations between
-    replays, equals the same rollout run eagerly."""
+    graph (policy, sampling, the C-ABI step and bookkeeping for all steps),
+    and the minibatch steps after the first update replay another.  Every
+    rollout replay, with the update replays and host synchronisations between
+    them, equals the same rollout run eagerly (eager updates)."""
     rom = synthrom.make_rom(5).rom
     snaps = warm_snapshots(rom, [100, 150, 200, 250], seed=55)
     for i, s in enumerate(snaps):
@@ -84,7 +85,7 @@ def test_rollout_graph_replays_match_eager_rollouts():
     n, T, updates = 64, 8, 4
     reward = dict(kind="x_delta", x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE,
                   clip=15, time_penalty=0.25)
-    runs = {}
+    runs, per_update = {}, {}
     for graph in (False, True):
         say(f"[gpu] ppo rollouts cuda_graph={graph}: N={n} T={T} updates={updates}")
         cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, n_steps=T, batch_size=128, update_epochs=1,
@@ -96,11 +97,63 @@ def test_rollout_graph_replays_match_eager_rollouts():
                                    on_rollout=lambda u, b: got.append(
                                        {k: (v.cpu().numpy().copy() if hasattr(v, "cpu") else v) for k, v in b.items()}))
         runs[graph] = got
+        per_update[graph] = stats["per_update"]
         assert stats["graph_updates"] == (updates - 1 if graph else 0)
     assert [r["graph"] for r in runs[True]] == [False] + [True] * (updates - 1)
+    assert [u["update_graph"] for u in per_update[True]] == [False] + [True] * (updates - 1)
+    assert not any(u["update_graph"] for u in per_update[False])
     for u, (e, g) in enumerate(zip(runs[False], runs[True])):
         for key in ("actions", "rewards", "dones"):
             np.testing.assert_array_equal(g[key], e[key], err_msg=f"update {u + 1} {key}")
         for key in ("values", "logprobs"):
             np.testing.assert_allclose(g[key], e[key], rtol=0, atol=1e-5, err_msg=f"update {u + 1} {key}")
     assert sum(int(r["dones"].sum()) for r in runs[True]) > 0
+
+
+def test_minibatch_graph_replays_match_eager_steps():
+    """One captured minibatch step (gather, forward, clipped loss, backward,
+    gradient-norm clipping, capturable Adam, loss sums) replayed per
+    minibatch, with eager work and host synchronisations between replays,
+    leaves the parameters, Adam's moments and step counters and the loss
+    sums equal to the same steps run eagerly, after every replay."""
+    torch_, _, Categorical = P._require_torch()
+    dev = torch.device("cuda")
+    B, count = 512, 2048
+    gen = torch.Generator().manual_seed(7)
+    src = {"obs": torch.randint(0, 256, (count, 2048), dtype=torch.uint8, generator=gen).to(dev),
+           "actions": torch.randint(0, 12, (count,), generator=gen).to(dev),
+           "logprobs": (-3.0 * torch.rand(count, generator=gen)).to(dev),
+           "advantages": torch.randn(count, generator=gen).to(dev),
+           "returns": torch.randn(count, generator=gen).to(dev)}
+    cfg = P.NativePPOConfig("synthetic.nes", batch_size=B)
+    updaters = []
+    for _ in range(2):
+        torch.manual_seed(3)
+        model = P._make_model(2048, 12, 256, "orthogonal", dev)
+        opt = torch.optim.Adam(model.parameters(), lr=cfg.learning_rate, eps=1e-5, capturable=True)
+        updaters.append(P.MinibatchUpdate(torch, Categorical, model, opt, cfg, src))
+    eager, graphed = updaters
+    idxs = [p[s:s + B] for p in (torch.randperm(count, generator=gen).to(dev) for _ in range(3))
+            for s in range(0, count, B)]
+    say(f"[gpu] ppo minibatch graph: B={B} count={count} steps={len(idxs)}")
+    eager.run(idxs[0])
+    graphed.run(idxs[0])
+    graphed.capture()
+    junk = torch.randn(512, 512, device=dev)
+    worst = 0.0
+    for k, idx in enumerate(idxs[1:], 1):
+        eager.run(idx)
+        graphed.run(idx)
+        junk = torch.tanh(junk @ junk)
+        torch.cuda.synchronize()
+        for (name, a), b in zip(eager.model.named_parameters(), graphed.model.parameters()):
+            worst = max(worst, float((a - b).abs().max()))
+            torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-6, msg=f"step {k} {name}")
+            sa, sb = eager.optimizer.state[a], graphed.optimizer.state[b]
+            for key in ("exp_avg", "exp_avg_sq", "step"):
+                torch.testing.assert_close(sb[key], sa[key], rtol=1e-5, atol=1e-9, msg=f"step {k} {name} {key}")
+        torch.testing.assert_close(graphed.sums, eager.sums, rtol=1e-5, atol=1e-6, msg=f"step {k} sums")
+    assert graphed.graph is not None and eager.graph is None
+    assert graphed.minibatches == eager.minibatches == len(idxs)
+    assert float(eager.sums.abs().sum()) > 0.0
+    say(f"[gpu] ppo minibatch graph: max parameter difference {worst:.3g}")

@@ -104,3 +104,27 @@ def test_checkpoint_round_trip_restores_rng_and_weights(tmp_path):
     torch.testing.assert_close(torch.rand(5), a_t)
     np.testing.assert_allclose(np.random.rand(5), a_n)
     torch.testing.assert_close(model2.weight, model.weight)
+
+
+def test_checkpoint_restores_adam_step_counters_where_the_trainer_keeps_them(tmp_path):
+    """A checkpoint keeps the flag its Adam was saved with; the trainer sets
+    ``capturable`` again after loading and moves the step counters to match
+    (device-side counters for the captured minibatch step)."""
+    torch.manual_seed(0)
+    model = P._make_model(2048, 7, 32, "orthogonal", torch.device("cpu"))
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3, eps=1e-5)
+    logits, value = model(torch.randint(0, 256, (4, 2048), dtype=torch.uint8))
+    (logits.sum() + value.sum()).backward()
+    opt.step()
+    path = tmp_path / "ckpt.pt"
+    P._save_checkpoint(str(path), model, opt, P.NativePPOConfig("rom.nes"), 77)
+    opt2 = torch.optim.Adam(model.parameters(), lr=1e-3, eps=1e-5, capturable=True)
+    assert P._load_checkpoint(str(path), model, opt2) == 77
+    assert all(not g["capturable"] for g in opt2.param_groups)      # the saved flag
+    P._set_capturable(torch, opt2, True)
+    assert all(g["capturable"] for g in opt2.param_groups)
+    for p in model.parameters():
+        step = opt2.state[p]["step"]
+        assert step.dtype == torch.float32 and step.device == p.device and float(step) == 1.0
+    P._set_capturable(torch, opt2, False)
+    assert all(opt2.state[p]["step"].device.type == "cpu" for p in model.parameters())
