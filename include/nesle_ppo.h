@@ -1,0 +1,52 @@
+/* nesle_ppo.h -- the clipped-PPO loss head of libnesle_hip.so.
+ *
+ * Plain C over device pointers: float32 tensors, int64 actions, work enqueued
+ * on the caller's HIP stream (nothing is allocated, nothing synchronises, no
+ * memset: the call may be captured in a graph).  Status codes and
+ * nesle_last_error() are those of nesle_hip.h.
+ */
+#ifndef NESLE_PPO_H
+#define NESLE_PPO_H
+
+#include <stdint.h>
+
+#include "nesle_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NESLE_PPO_MAX_ACTIONS 1024u
+
+/* Floats of scratch nesle_ppo_head needs for a minibatch of `batch` rows. */
+uint32_t nesle_ppo_head_scratch_floats(uint32_t batch);
+
+/* The loss of one PPO minibatch and its gradient, replacing the loss lines
+ * of the reference trainer (src/nesle/native_ppo.py:546-566: Categorical
+ * log-probability and entropy of `logits`, ratio against `old_logprob`,
+ * advantages normalised by their mean and unbiased standard deviation + 1e-8,
+ * the clipped surrogate max(-A r, -A clamp(r, 1 - clip, 1 + clip)), the value
+ * loss 0.5 (value - return)^2, all as means over the rows; loss =
+ * surrogate - ent_coef * entropy + vf_coef * value loss).
+ *
+ *   logits [batch, num_actions], value [batch], actions [batch] (int64, in
+ *   0..num_actions-1; another value makes that row's terms NaN),
+ *   old_logprob, advantages, returns [batch]: inputs, contiguous.
+ *   dlogits [batch, num_actions], dvalue [batch]: d loss / d input for a
+ *   loss gradient of 1 (the autograd backward scales them).
+ *   scratch: nesle_ppo_head_scratch_floats(batch) floats.
+ *   loss, clipfrac: one float each (clipfrac = mean of |r - 1| > clip).
+ *   accum: null, or two floats to which loss and clipfrac are added.
+ *
+ * Fails with NESLE_EINVAL for batch 0, num_actions outside
+ * 1..NESLE_PPO_MAX_ACTIONS or a null pointer (other than accum). */
+int nesle_ppo_head(const float* logits, const float* value, const int64_t* actions, const float* old_logprob,
+                   const float* advantages, const float* returns, uint32_t batch, uint32_t num_actions,
+                   double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
+                   float* scratch, float* loss, float* clipfrac, float* accum, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NESLE_PPO_H */

@@ -18,7 +18,8 @@ import numpy as np
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libnesle_hip.so"
-HEADER = PKG.parent / "include" / "nesle_hip.h"
+INCLUDE = PKG.parent / "include"
+HEADER = INCLUDE / "nesle_hip.h"
 
 OK, EINVAL, ERUNTIME, EDEVICE = 0, 1, 2, 3
 REWARD_SMB, REWARD_XDELTA = 0, 1
@@ -83,10 +84,12 @@ def bind_runtime() -> None:
 
 
 def declared_functions() -> list[str]:
-    """Names of every function include/nesle_hip.h declares."""
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(nesle_[a-z0-9_]+)\s*\(", text)))
+    """Names of every function the headers under include/ declare."""
+    names: set[str] = set()
+    for header in sorted(INCLUDE.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(nesle_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def lib():
@@ -130,6 +133,9 @@ def lib():
         "nesle_parse_ines": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(RomInfo)]),
         "nesle_parse_fcs": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, _U8P]),
         "nesle_last_error": (ctypes.c_char_p, []),
+        "nesle_ppo_head_scratch_floats": (ctypes.c_uint32, [ctypes.c_uint32]),
+        "nesle_ppo_head": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double,
+                                          ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -26,7 +26,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnesle_hip.so"
-HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_kernels.hip", CSRC / "nes_render.hip", CSRC / "nes_host.hip"]
+HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_kernels.hip", CSRC / "nes_render.hip", CSRC / "nes_host.hip",
+               CSRC / "ppo_head.hip"]
 SHIM_SOURCE = CSRC / "cuda_core_module.cpp"
 
 HIP_FLAGS = [

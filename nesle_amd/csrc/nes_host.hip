@@ -392,6 +392,8 @@ struct nesle_batch {
     }
 };
 
+void nesle::set_last_error(const std::string& msg) { g_error = msg; }
+
 extern "C" {
 
 const char* nesle_last_error(void) { return g_error.c_str(); }

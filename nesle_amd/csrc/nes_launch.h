@@ -1,9 +1,11 @@
-// nes_launch.h -- host-side launchers for the kernels in nes_kernels.hip.
+// nes_launch.h -- host-side launchers for the kernels in nes_kernels.hip, and the
+// error message shared by every C entry point.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <string>
 
 #include "nes_layout.h"
 
@@ -23,5 +25,9 @@ hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32
 hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
 // Presentation snapshot (and pre-render latch) from live state, masked.
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
+
+// The calling thread's message for nesle_last_error(), from entry points
+// outside the batch (nes_host.hip keeps it).
+void set_last_error(const std::string& msg);
 
 }  // namespace nesle

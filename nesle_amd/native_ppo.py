@@ -246,34 +246,108 @@ def _capture_rollout(torch, batch, rollout_step, T: int, model, ram):
     return graph
 
 
-def _set_capturable(torch, optimizer, capturable: bool) -> None:
-    """Adam with its step counters on the device (``capturable``) runs inside
-    a captured graph; a checkpoint restores the flag it was saved with, so it
-    is set again after loading and the counters are moved to match."""
+def _configure_adam(torch, optimizer) -> None:
+    """The trainer's Adam runs fused (one kernel per step) with its step
+    counters on the device (``capturable``, which the captured minibatch step
+    needs).  A checkpoint restores the flags it was saved with, so they are
+    set again after loading and the counters moved to match."""
     for group in optimizer.param_groups:
-        group["capturable"] = capturable
+        group["capturable"] = True
+        group["fused"] = True
+        group["foreach"] = None
         for p in group["params"]:
             state = optimizer.state.get(p)
             if state and "step" in state:
-                device = p.device if capturable else torch.device("cpu")
-                state["step"] = state["step"].to(dtype=torch.float32, device=device)
+                state["step"] = state["step"].to(dtype=torch.float32, device=p.device)
+
+
+_PPO_HEAD = None
+
+
+def ppo_head_loss(logits, value, actions, old_logprob, advantages, returns, clip_coef: float, ent_coef: float,
+                  vf_coef: float, accum=None):
+    """(loss, clip fraction) of one minibatch by the HIP loss head
+    (``nesle_ppo_head``, include/nesle_ppo.h): the reference's loss lines
+    (native_ppo.py:546-566) in three kernels, with d loss / d logits and
+    d loss / d value computed in the same pass and returned by the autograd
+    backward.  Every tensor must live on the GPU (contiguous float32, int64
+    actions); ``accum`` (two floats on the GPU) receives loss and clip
+    fraction added to it."""
+    global _PPO_HEAD
+    torch, _, _ = _require_torch()
+    if _PPO_HEAD is None:
+        _PPO_HEAD = _make_ppo_head(torch)
+    return _PPO_HEAD.apply(logits, value, actions, old_logprob, advantages, returns, float(clip_coef),
+                           float(ent_coef), float(vf_coef), accum)
+
+
+def _make_ppo_head(torch):
+    from nesle_amd import abi
+
+    L = abi.lib()
+
+    def need(t, name, dtype, shape):
+        if not (t.is_cuda and t.dtype == dtype and tuple(t.shape) == shape and t.is_contiguous()):
+            raise ValueError(f"ppo_head_loss: {name} must be a contiguous {dtype} GPU tensor of shape {shape}, "
+                             f"got {tuple(t.shape)} {t.dtype} on {t.device}")
+
+    class PPOHead(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, logits, value, actions, old_logprob, advantages, returns, clip_coef, ent_coef, vf_coef,
+                    accum):
+            if logits.dim() != 2:
+                raise ValueError("ppo_head_loss: logits must be [batch, actions]")
+            n, a = logits.shape
+            need(logits, "logits", torch.float32, (n, a))
+            need(value, "value", torch.float32, (n,))
+            need(actions, "actions", torch.int64, (n,))
+            for t, name in ((old_logprob, "old_logprob"), (advantages, "advantages"), (returns, "returns")):
+                need(t, name, torch.float32, (n,))
+            if accum is not None:
+                need(accum, "accum", torch.float32, (2,))
+            dev = logits.device
+            if any(t.device != dev for t in (value, actions, old_logprob, advantages, returns)):
+                raise ValueError("ppo_head_loss: all tensors must be on one device")
+            dlogits = torch.empty_like(logits)
+            dvalue = torch.empty_like(value)
+            scratch = torch.empty(int(L.nesle_ppo_head_scratch_floats(n)), dtype=torch.float32, device=dev)
+            loss = torch.empty((), dtype=torch.float32, device=dev)
+            clipfrac = torch.empty((), dtype=torch.float32, device=dev)
+            with torch.cuda.device(dev):
+                stream = torch.cuda.current_stream(dev).cuda_stream
+                abi._check(L.nesle_ppo_head(
+                    logits.data_ptr(), value.data_ptr(), actions.data_ptr(), old_logprob.data_ptr(),
+                    advantages.data_ptr(), returns.data_ptr(), n, a, clip_coef, ent_coef, vf_coef,
+                    dlogits.data_ptr(), dvalue.data_ptr(), scratch.data_ptr(), loss.data_ptr(), clipfrac.data_ptr(),
+                    accum.data_ptr() if accum is not None else None, stream))
+            ctx.grads = (dlogits, dvalue)
+            ctx.mark_non_differentiable(clipfrac)
+            return loss, clipfrac
+
+        @staticmethod
+        def backward(ctx, g_loss, g_clipfrac):
+            dlogits, dvalue = ctx.grads
+            return dlogits * g_loss, dvalue * g_loss, None, None, None, None, None, None, None, None
+
+    return PPOHead
 
 
 class MinibatchUpdate:
     """Clipped-PPO minibatch steps over the rollout buffers
-    (native_ppo.py:540-575): forward, loss, backward, gradient-norm clipping
-    and Adam, with the loss and clip fraction summed on the device.
+    (native_ppo.py:540-575): forward, the loss head (``ppo_head_loss``),
+    backward, gradient-norm clipping and Adam, with the loss and clip fraction
+    summed on the device.
 
     ``run(idx)`` takes one minibatch of sample indices.  After ``capture()``
     a full minibatch replays one HIP graph of the whole step instead (about
-    60 launches each): ``idx`` is copied into the graph's index buffer and
-    the graph gathers the minibatch from ``sources``, whose device buffers
-    must stay in place.  The captured work holds no host synchronisation
-    (the distribution skips argument validation, clipping is a device-side
-    scale, Adam is ``capturable``)."""
+    40 launches): ``idx`` is copied into the graph's index buffer and the
+    graph gathers the minibatch from ``sources``, whose device buffers must
+    stay in place.  The captured work holds no host synchronisation (the
+    loss head runs no memset and reads nothing back, clipping is a
+    device-side scale, Adam is fused and ``capturable``)."""
 
-    def __init__(self, torch, Categorical, model, optimizer, config: NativePPOConfig, sources: dict):
-        self.torch, self.Categorical = torch, Categorical
+    def __init__(self, torch, model, optimizer, config: NativePPOConfig, sources: dict):
+        self.torch = torch
         self.model, self.optimizer, self.config = model, optimizer, config
         self.sources = sources          # obs, actions, logprobs, advantages, returns: [count, ...]
         dev = sources["obs"].device
@@ -282,29 +356,18 @@ class MinibatchUpdate:
         self.idx = torch.zeros(config.batch_size, dtype=torch.long, device=dev)
         self.graph = None
 
-    def _loss(self, idx):
-        torch, cfg, src = self.torch, self.config, self.sources
+    def _loss(self, idx, accum=None):
+        cfg, src = self.config, self.sources
         logits, newvalue = self.model(src["obs"][idx])
-        dist = self.Categorical(logits=logits, validate_args=False)
-        newlogprob = dist.log_prob(src["actions"][idx])
-        entropy = dist.entropy().mean()
-        ratio = (newlogprob - src["logprobs"][idx]).exp()
-        adv = src["advantages"][idx]
-        adv = (adv - adv.mean()) / (adv.std() + 1e-8)
-        pg_loss = torch.max(-adv * ratio, -adv * torch.clamp(ratio, 1.0 - cfg.clip_coef, 1.0 + cfg.clip_coef)).mean()
-        value_loss = 0.5 * (newvalue - src["returns"][idx]).pow(2).mean()
-        return pg_loss - cfg.ent_coef * entropy + cfg.vf_coef * value_loss, ratio
+        return ppo_head_loss(logits, newvalue, src["actions"][idx], src["logprobs"][idx], src["advantages"][idx],
+                             src["returns"][idx], cfg.clip_coef, cfg.ent_coef, cfg.vf_coef, accum)
 
     def _step(self, idx) -> None:
-        torch = self.torch
-        loss, ratio = self._loss(idx)
+        loss, _ = self._loss(idx, self.sums)
         self.optimizer.zero_grad(set_to_none=True)
         loss.backward()
-        torch.nn.utils.clip_grad_norm_(self.model.parameters(), self.config.max_grad_norm)
+        self.torch.nn.utils.clip_grad_norm_(self.model.parameters(), self.config.max_grad_norm)
         self.optimizer.step()
-        with torch.no_grad():
-            clipfrac = ((ratio - 1.0).abs() > self.config.clip_coef).float().mean()
-            self.sums.add_(torch.stack([loss.detach(), clipfrac]))
 
     def run(self, idx) -> None:
         if self.graph is not None and idx.shape[0] == self.idx.shape[0]:
@@ -364,7 +427,7 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     if config.reward_mode != "minimal":
         raise ValueError(f"reward_mode {config.reward_mode!r} is not provided: only 'minimal' "
                          "(the batch's in-kernel reward rule)")
-    torch, _, Categorical = _require_torch()
+    torch, _, _ = _require_torch()
     if not torch.cuda.is_available():
         raise SystemExit("native PPO needs a GPU")
     torch.manual_seed(config.seed)
@@ -382,12 +445,12 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     dev = torch.device("cuda")
     obs_dim, action_dim, n = 2048, len(masks), config.num_envs
     model = _make_model(obs_dim, action_dim, config.hidden_size, config.init, dev)
-    # Adam keeps its step counters on the device in both modes (the captured
-    # minibatch step needs it), so eager and graph training compute the same
-    # numbers.
-    optimizer = torch.optim.Adam(model.parameters(), lr=config.learning_rate, eps=1e-5, capturable=True)
+    # Fused Adam with its step counters on the device in both modes (the
+    # captured minibatch step needs them), so eager and graph training compute
+    # the same numbers.
+    optimizer = torch.optim.Adam(model.parameters(), lr=config.learning_rate, eps=1e-5, capturable=True, fused=True)
     global_step = _load_checkpoint(resume_from, model, optimizer)
-    _set_capturable(torch, optimizer, True)
+    _configure_adam(torch, optimizer)
     resume_step = global_step
     mask_table = torch.tensor(masks, dtype=torch.uint8, device=dev)
 
@@ -446,7 +509,7 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         episode_returns.mul_(keep)
         episode_lengths.mul_(keep)
 
-    updater = MinibatchUpdate(torch, Categorical, model, optimizer, config, {
+    updater = MinibatchUpdate(torch, model, optimizer, config, {
         "obs": obs_buf.reshape((-1, obs_dim)), "actions": actions_buf.reshape(-1),
         "logprobs": logprobs_buf.reshape(-1), "advantages": adv_buf.reshape(-1), "returns": ret_buf.reshape(-1)})
     update_graph_ok = config.cuda_graph and rollout_timesteps % config.batch_size == 0

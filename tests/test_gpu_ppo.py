@@ -111,12 +111,11 @@ def test_rollout_graph_replays_match_eager_rollouts():
 
 
 def test_minibatch_graph_replays_match_eager_steps():
-    """One captured minibatch step (gather, forward, clipped loss, backward,
-    gradient-norm clipping, capturable Adam, loss sums) replayed per
+    """One captured minibatch step (gather, forward, the HIP loss head,
+    backward, gradient-norm clipping, fused capturable Adam) replayed per
     minibatch, with eager work and host synchronisations between replays,
     leaves the parameters, Adam's moments and step counters and the loss
     sums equal to the same steps run eagerly, after every replay."""
-    torch_, _, Categorical = P._require_torch()
     dev = torch.device("cuda")
     B, count = 512, 2048
     gen = torch.Generator().manual_seed(7)
@@ -130,8 +129,8 @@ def test_minibatch_graph_replays_match_eager_steps():
     for _ in range(2):
         torch.manual_seed(3)
         model = P._make_model(2048, 12, 256, "orthogonal", dev)
-        opt = torch.optim.Adam(model.parameters(), lr=cfg.learning_rate, eps=1e-5, capturable=True)
-        updaters.append(P.MinibatchUpdate(torch, Categorical, model, opt, cfg, src))
+        opt = torch.optim.Adam(model.parameters(), lr=cfg.learning_rate, eps=1e-5, capturable=True, fused=True)
+        updaters.append(P.MinibatchUpdate(torch, model, opt, cfg, src))
     eager, graphed = updaters
     idxs = [p[s:s + B] for p in (torch.randperm(count, generator=gen).to(dev) for _ in range(3))
             for s in range(0, count, B)]
@@ -147,7 +146,7 @@ def test_minibatch_graph_replays_match_eager_steps():
         junk = torch.tanh(junk @ junk)
         torch.cuda.synchronize()
         for (name, a), b in zip(eager.model.named_parameters(), graphed.model.parameters()):
-            worst = max(worst, float((a - b).abs().max()))
+            worst = max(worst, float((a.detach() - b.detach()).abs().max()))
             torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-6, msg=f"step {k} {name}")
             sa, sb = eager.optimizer.state[a], graphed.optimizer.state[b]
             for key in ("exp_avg", "exp_avg_sq", "step"):
@@ -157,3 +156,66 @@ def test_minibatch_graph_replays_match_eager_steps():
     assert graphed.minibatches == eager.minibatches == len(idxs)
     assert float(eager.sums.abs().sum()) > 0.0
     say(f"[gpu] ppo minibatch graph: max parameter difference {worst:.3g}")
+
+
+def _reference_loss(logits, value, actions, old_logprob, advantages, returns, clip, ent_coef, vf_coef):
+    """The reference trainer's loss lines (native_ppo.py:546-566), float32."""
+    from torch.distributions.categorical import Categorical
+
+    dist = Categorical(logits=logits)
+    newlogprob = dist.log_prob(actions)
+    entropy = dist.entropy().mean()
+    ratio = (newlogprob - old_logprob).exp()
+    adv = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
+    pg_loss = torch.max(-adv * ratio, -adv * torch.clamp(ratio, 1.0 - clip, 1.0 + clip)).mean()
+    value_loss = 0.5 * (value - returns).pow(2).mean()
+    loss = pg_loss - ent_coef * entropy + vf_coef * value_loss
+    clipfrac = ((ratio - 1.0).abs() > clip).float().mean()
+    return loss, clipfrac
+
+
+@pytest.mark.parametrize("n,a,spread", [(8192, 12, 0.3), (300, 256, 0.05), (1000, 7, 0.0), (2, 1, 0.2)])
+def test_ppo_head_matches_the_reference_loss_and_its_gradients(n, a, spread):
+    """The HIP loss head (nesle_ppo_head) against the reference's loss
+    computed by PyTorch autograd in float32 on the host: loss, clip fraction,
+    d loss / d logits and d loss / d value, for a loss gradient of 1 and of
+    -2.5.  Rows mix ratios inside and outside the clip range (spread 0:
+    every ratio exactly 1, the tie of the two surrogate terms), zero
+    advantages, and batches that are not a multiple of the head's 256-row
+    workgroup.  Tolerance 1e-5 relative on the loss, 1e-4 relative +
+    1e-7 absolute per gradient element (float32 sums in another order)."""
+    gen = torch.Generator().manual_seed(n * 7 + a)
+    logits = 3.0 * torch.randn(n, a, generator=gen)
+    value = torch.randn(n, generator=gen)
+    actions = torch.randint(0, a, (n,), generator=gen)
+    logp = torch.log_softmax(logits, dim=-1).gather(1, actions[:, None]).squeeze(1)
+    old_logprob = logp + spread * torch.randn(n, generator=gen)
+    if spread == 0.0:
+        old_logprob = logp.clone()
+    advantages = torch.randn(n, generator=gen)
+    advantages[::5] = 0.0
+    returns = torch.randn(n, generator=gen)
+    say(f"[gpu] ppo head: n={n} actions={a} spread={spread}")
+    clip, ent_coef, vf_coef = 0.1, 0.01, 0.5
+    dev = torch.device("cuda")
+    for scale in (1.0, -2.5):
+        ref_l = logits.clone().requires_grad_(True)
+        ref_v = value.clone().requires_grad_(True)
+        want_loss, want_cf = _reference_loss(ref_l, ref_v, actions, old_logprob, advantages, returns, clip, ent_coef,
+                                             vf_coef)
+        (scale * want_loss).backward()
+        gl = logits.to(dev).requires_grad_(True)
+        gv = value.to(dev).requires_grad_(True)
+        accum = torch.tensor([1.0, 2.0], device=dev)
+        loss, cf = P.ppo_head_loss(gl, gv, actions.to(dev), old_logprob.to(dev), advantages.to(dev),
+                                   returns.to(dev), clip, ent_coef, vf_coef, accum)
+        (scale * loss).backward()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(loss.detach().cpu(), want_loss.detach(), rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(cf.cpu(), want_cf, rtol=0, atol=0.5 / n)
+        torch.testing.assert_close(accum.cpu(), torch.stack([1.0 + want_loss.detach(), 2.0 + want_cf]),
+                                   rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(gl.grad.cpu(), ref_l.grad, rtol=1e-4, atol=1e-7)
+        torch.testing.assert_close(gv.grad.cpu(), ref_v.grad, rtol=1e-4, atol=1e-7)
+    if spread == 0.0:
+        assert float(want_cf) == 0.0

@@ -106,10 +106,11 @@ def test_checkpoint_round_trip_restores_rng_and_weights(tmp_path):
     torch.testing.assert_close(model2.weight, model.weight)
 
 
-def test_checkpoint_restores_adam_step_counters_where_the_trainer_keeps_them(tmp_path):
-    """A checkpoint keeps the flag its Adam was saved with; the trainer sets
-    ``capturable`` again after loading and moves the step counters to match
-    (device-side counters for the captured minibatch step)."""
+def test_checkpoint_restores_adam_to_the_trainer_configuration(tmp_path):
+    """A checkpoint keeps the flags its Adam was saved with (the reference's
+    plain Adam: host step counters); the trainer sets fused and capturable
+    again after loading and moves the step counters to the parameters'
+    device as float32."""
     torch.manual_seed(0)
     model = P._make_model(2048, 7, 32, "orthogonal", torch.device("cpu"))
     opt = torch.optim.Adam(model.parameters(), lr=1e-3, eps=1e-5)
@@ -118,13 +119,36 @@ def test_checkpoint_restores_adam_step_counters_where_the_trainer_keeps_them(tmp
     opt.step()
     path = tmp_path / "ckpt.pt"
     P._save_checkpoint(str(path), model, opt, P.NativePPOConfig("rom.nes"), 77)
-    opt2 = torch.optim.Adam(model.parameters(), lr=1e-3, eps=1e-5, capturable=True)
+    opt2 = torch.optim.Adam(model.parameters(), lr=1e-3, eps=1e-5, capturable=True, fused=True)
     assert P._load_checkpoint(str(path), model, opt2) == 77
-    assert all(not g["capturable"] for g in opt2.param_groups)      # the saved flag
-    P._set_capturable(torch, opt2, True)
-    assert all(g["capturable"] for g in opt2.param_groups)
+    assert all(not g["capturable"] and not g["fused"] for g in opt2.param_groups)      # the saved flags
+    P._configure_adam(torch, opt2)
+    assert all(g["capturable"] and g["fused"] for g in opt2.param_groups)
     for p in model.parameters():
         step = opt2.state[p]["step"]
         assert step.dtype == torch.float32 and step.device == p.device and float(step) == 1.0
-    P._set_capturable(torch, opt2, False)
-    assert all(opt2.state[p]["step"].device.type == "cpu" for p in model.parameters())
+    for p in model.parameters():
+        p.grad = torch.ones_like(p)
+    opt2.step()
+    assert all(float(opt2.state[p]["step"]) == 2.0 for p in model.parameters())
+
+
+def test_ppo_head_refuses_host_tensors_before_any_launch():
+    """The HIP loss head takes device pointers only: host tensors, wrong
+    dtypes or shapes are rejected in Python, and the C entry point rejects
+    bad sizes and null pointers before it launches anything."""
+    from nesle_amd import abi
+
+    n, a = 8, 5
+    args = [torch.zeros(n, a), torch.zeros(n), torch.zeros(n, dtype=torch.int64), torch.zeros(n), torch.zeros(n),
+            torch.zeros(n)]
+    with pytest.raises(ValueError, match="GPU tensor"):
+        P.ppo_head_loss(*args, 0.1, 0.01, 0.5)
+    L = abi.lib()
+    assert L.nesle_ppo_head_scratch_floats(8192) == 2 + 4 * 32
+    assert L.nesle_ppo_head_scratch_floats(257) == 2 + 4 * 2
+    for batch, actions in ((0, 12), (16, 0), (16, 1025)):
+        assert L.nesle_ppo_head(*([None] * 6), batch, actions, 0.1, 0.01, 0.5, *([None] * 7)) == abi.EINVAL
+        assert b"num_actions" in L.nesle_last_error()
+    assert L.nesle_ppo_head(*([None] * 6), 16, 12, 0.1, 0.01, 0.5, *([None] * 7)) == abi.EINVAL
+    assert b"null" in L.nesle_last_error()
