@@ -1,5 +1,5 @@
 """The C ABI of libnesle_hip.so without a GPU: the library loads, exports every
-function include/nesle_hip.h declares, and its host-only entry points
+function the headers under include/ declare, and its host-only entry points
 (iNES/FCS parsing, argument validation) behave like the reference binding's
 (cpp/src/rom.cpp:65-121, cpp/bindings/cuda_module.cu:371-376)."""
 
