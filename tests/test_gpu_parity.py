@@ -155,6 +155,49 @@ def test_snapshot_autoreset_xdelta_reward():
     assert (np.unique(b.host(abi.VIEW_REWARDS)) <= 15 - 0.25).all()
 
 
+def test_benchmark_configuration_full_size_sampled():
+    """The benchmark's configuration at full size: 65,536 consoles (RAM rows
+    split between LDS and HBM), 8 snapshot levels spread at random, x-delta
+    reward with time penalty and fused auto-reset.  Sampled consoles (edges of
+    waves, workgroups and XCD ranges, random ones) have the rewards and dones
+    of the oracle restoring the same snapshot after every step, and its state
+    every third step; episodes end within the run."""
+    rom = synthrom.make_rom(5).rom
+    snaps = warm_snapshots(rom, [100, 150, 200, 250, 300, 350, 400, 450], seed=55)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 1 + (i % 3)  # done after at most 3 frames x 8
+    blobs = [bytes(s) for s in snaps]
+    n, steps = 65536, 9
+    rng = np.random.default_rng(2026)
+    levels = rng.integers(0, 8, n).astype(np.uint8)
+    sample = sorted({0, 1, 63, 64, 255, 256, 8191, 8192, 32768, n - 1, *rng.integers(0, n, 8).tolist()})
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.01)
+    say(f"[gpu] benchmark configuration: N={n} fs=4 steps={steps} sample={sample}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.01)
+    b.set_snapshots(blobs, levels)
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        c.load(snaps[levels[e]])
+    ends = 0
+    for k in range(steps):
+        m = masks_for(4242, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES)[sample], don, err_msg=f"step {k} dones")
+        for j in np.nonzero(don)[0]:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += int(don.sum())
+        if k % 3 == 2:
+            for e, ref in zip(sample, ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert ends >= len(sample)
+
+
 def test_reset_envs_and_state_roundtrip():
     """Masked reset returns exactly the selected consoles to power-on; a saved
     state loaded into other consoles makes them identical; int64 device
