@@ -30,7 +30,8 @@ HBM bytes per launch that rocprofv3 measured (FETCH_SIZE and WRITE_SIZE,
 scaled by a copy-kernel calibration) in profiles/step_kernel_65536_fs4.md.
 ``roofline_valu`` gives the emulated 6502 instruction rate and the VALU pipe
 busy fraction from the same profile (SQ_INSTS_VALU x 4 cycles over 1,024
-SIMDs and the kernel time).
+SIMDs and the kernel time).  ``by_size`` repeats these figures, with NES
+frames/s, for 4,096 and 65,536 consoles.
 
 ``cpu_baseline``: the reference's own CPU core (``nesle::Console`` compiled
 from the reference sources into oracle/_ref) on the host's cores, one console
@@ -76,6 +77,28 @@ def profile_figure(key: str, num_envs: int) -> float | None:
         if len(parts) == 3 and parts[0] == key and parts[1] == str(num_envs):
             return float(parts[2])
     return None
+
+
+def size_figures(run: dict, num_envs: int) -> dict:
+    """Throughput and roofline fractions of one batch size: NES frames/s,
+    algorithmic and measured (rocprofv3, committed summary) HBM bytes per
+    kernel time against the 8 TB/s peak, and the VALU pipe's busy fraction."""
+    kernel_s = run["kernel_ms_per_launch"] / 1000.0
+    algo = num_envs * B_STEP / kernel_s / 1e9
+    traffic = profile_figure("traffic_bytes_per_launch", num_envs)
+    measured = traffic / kernel_s / 1e9 if traffic else None
+    return {
+        "num_envs": num_envs,
+        "env_steps_per_s": run["env_steps_per_s"],
+        "nes_frames_per_s": 4 * run["env_steps_per_s"],
+        "kernel_ms_per_launch": run["kernel_ms_per_launch"],
+        "emulated_instr_per_s": run["instructions_per_env_step"] * num_envs / kernel_s,
+        "hbm_algorithmic_gbs": algo,
+        "hbm_algorithmic_frac": algo / HBM_PEAK_GBS,
+        "hbm_measured_gbs": measured,
+        "hbm_measured_frac": measured / HBM_PEAK_GBS if measured else None,
+        "valu_busy_frac": profile_figure("valu_busy", num_envs),
+    }
 
 
 def log(msg: str) -> None:
@@ -367,6 +390,7 @@ def main() -> int:
             "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
         },
+        "by_size": [size_figures(small, args.small_envs), size_figures(big, args.envs)],
         "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel, "ppo_8192x128": ppo,
                   "vec_env_ram_4096": vec},
     }
