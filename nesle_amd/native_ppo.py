@@ -740,6 +740,7 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
              "wall_s": 0.0, "log": [], "per_update": [], "graph_updates": 0}
     graph = None
     step_ms = None   # step-kernel time per rollout step, from the eager first rollout
+    progress = _progress_bar(config.progress_bar, global_step + num_updates * rollout_timesteps, global_step)
     t_start = time.perf_counter()
     for update in range(1, num_updates + 1):
         # The first rollout runs eagerly (HIP-event timing of the step kernel,
@@ -762,6 +763,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 if record is not None:
                     record(t, mask_table[actions_buf[t]], rewards_buf[t], next_done.bool())
         global_step += rollout_timesteps
+        if progress is not None:
+            progress.update(rollout_timesteps)   # per rollout: the steps run inside one graph
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         if not use_graph:
@@ -812,18 +815,36 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 "ep_len_mean": fin[2] / fin[0] if fin[0] else float("nan"),
             }
             stats["log"].append(line)
+            if progress is not None:
+                progress.set_postfix(fps=line["fps"], ret=f"{line['ep_return_mean']:.1f}",
+                                     ev=f"{line['explained_var']:.2f}", clip=f"{line['clipfrac']:.2f}")
             print(f"update={update}/{num_updates} step={global_step} fps={line['fps']} loss={line['loss']:.4f} "
                   f"clipfrac={line['clipfrac']:.3f} explained_var={line['explained_var']:.3f} "
                   f"episodes={line['episodes']} ep_return={line['ep_return_mean']:.2f}", flush=True)
             if config.save_checkpoints:
                 _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     torch.cuda.synchronize()
+    if progress is not None:
+        progress.close()
     stats["wall_s"] = time.perf_counter() - t_start
     stats["global_step"] = global_step
     if config.save_checkpoints and num_updates > 0:
         _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     stats["model"] = model
     return stats
+
+
+def _progress_bar(enabled: bool, total: int, initial: int):
+    """A tqdm bar over env-steps when asked for and tqdm is importable
+    (native_ppo.py:606-613)."""
+    if not enabled:
+        return None
+    try:
+        from tqdm.auto import tqdm
+    except ImportError:
+        print("progress bar requested but tqdm is not installed; falling back to update logs")
+        return None
+    return tqdm(total=total, initial=min(initial, total), desc="native PPO", unit="steps")
 
 
 def parse_args() -> tuple[NativePPOConfig, str | None]:
@@ -859,6 +880,7 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
     p.add_argument("--checkpoint-path", default="nesle_native_ppo.pt")
     p.add_argument("--resume-from", default=None)
     p.add_argument("--log-interval", type=int, default=1)
+    p.add_argument("--progress-bar", action="store_true")
     a = p.parse_args()
     if a.reset_state_path and a.reset_state_paths:
         raise SystemExit("Pass either --reset-state-path or --reset-state-paths, not both.")
@@ -870,7 +892,7 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
         gae_lambda=a.gae_lambda, clip_coef=a.clip_coef, ent_coef=a.ent_coef, vf_coef=a.vf_coef,
         max_grad_norm=a.max_grad_norm, hidden_size=a.hidden_size, reward_mode=a.reward_mode,
         flag_bonus=a.flag_bonus, finish_zone_bonus=a.finish_zone_bonus, death_penalty=a.death_penalty, init=a.init,
-        seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval)
+        seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval, progress_bar=a.progress_bar)
     return cfg, a.resume_from
 
 
