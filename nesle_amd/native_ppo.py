@@ -803,7 +803,11 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         stats["emulator_s"] += emu
 
         if update % max(1, config.log_interval) == 0 or update == num_updates:
+            # Episodes finished since the previous log line (the reference
+            # averages the last 100, read back every step).
             fin = [float(fin_count.sum()), float(fin_return.sum()), float(fin_length.sum())]
+            for acc in (fin_count, fin_return, fin_length):
+                acc.zero_()
             mean_loss, mean_clipfrac = updater.means()
             elapsed = max(1e-6, time.perf_counter() - t_start)
             line = {
@@ -820,7 +824,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                                      ev=f"{line['explained_var']:.2f}", clip=f"{line['clipfrac']:.2f}")
             print(f"update={update}/{num_updates} step={global_step} fps={line['fps']} loss={line['loss']:.4f} "
                   f"clipfrac={line['clipfrac']:.3f} explained_var={line['explained_var']:.3f} "
-                  f"episodes={line['episodes']} ep_return={line['ep_return_mean']:.2f}", flush=True)
+                  f"episodes={line['episodes']} ep_return={line['ep_return_mean']:.2f} "
+                  f"ep_len={line['ep_len_mean']:.1f}", flush=True)
             if config.save_checkpoints:
                 _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     torch.cuda.synchronize()
