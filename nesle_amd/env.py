@@ -224,8 +224,9 @@ class NesleVecEnv(_VecEnvBase):
         return core.CudaBatch(self.num_envs, self.frameskip, rom, snapshots, levels)
 
     def _infos(self, **extra) -> list[dict[str, Any]]:
-        return [{"backend": BACKEND_NAME, "observation_mode": self.observation_mode, **extra}
-                for _ in range(self.num_envs)]
+        base = {"backend": BACKEND_NAME, "observation_mode": self.observation_mode, **extra}
+        copy = base.copy
+        return [copy() for _ in range(self.num_envs)]
 
     def _masks_for(self, actions: Iterable[int]) -> np.ndarray:
         a = np.asarray(actions, dtype=np.int64).ravel()
@@ -275,10 +276,14 @@ class NesleVecEnv(_VecEnvBase):
 
     def _finish_episodes(self, dones, truncated, terminal: np.ndarray, infos) -> None:
         """Record terminal observations, reset done envs on the device."""
-        for env in np.nonzero(dones)[0]:
-            infos[env]["terminal_observation"] = terminal[env].copy()
-            infos[env]["terminated"] = bool(not truncated[env])
-            infos[env]["truncated"] = bool(truncated[env])
+        done_envs = np.nonzero(dones)[0]
+        # One gathered copy per step; each info holds its console's row of it.
+        last = terminal[done_envs]
+        for i, env in enumerate(done_envs.tolist()):
+            info = infos[env]
+            info["terminal_observation"] = last[i]
+            info["terminated"] = not bool(truncated[env])
+            info["truncated"] = bool(truncated[env])
             self.reset_infos[env] = {"backend": BACKEND_NAME, "observation_mode": self.observation_mode}
         self._cuda_batch.reset_envs(dones.astype(np.uint8))
         self._cuda_env_step_counts[dones] = 0
