@@ -31,7 +31,9 @@ HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_kernels.hip", CSRC / "nes_rend
 SHIM_SOURCE = CSRC / "cuda_core_module.cpp"
 
 HIP_FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
+    # -O2: the step kernel runs about 1 % faster than at -O3 (65,536 consoles,
+    # same-box A/B), the renderer and the PPO head no slower.
+    "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
     # Keep the compiler from forming packed fp32 VALU ops.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
