@@ -16,9 +16,28 @@ touches a GPU; using them without the built libraries raises ImportError.
 
 from __future__ import annotations
 
-__all__ = ["load_cuda_core", "make_vec", "synthrom", "abi"]
+__version__ = "0.1.0"
 
 from . import abi, synthrom  # noqa: F401
+from .actions import (  # noqa: F401  (the reference package exports these at its root)
+    COMPLEX_MOVEMENT,
+    COMPLEX_MOVEMENT_MASKS,
+    MARIO_MOVEMENT,
+    MARIO_MOVEMENT_MASKS,
+    RIGHT_ONLY,
+    RIGHT_ONLY_MASKS,
+    SIMPLE_MOVEMENT,
+    SIMPLE_MOVEMENT_MASKS,
+    SIMPLE_MOVEMENT_WITH_START,
+    SIMPLE_MOVEMENT_WITH_START_MASKS,
+    Button,
+    encode_action,
+)
+
+__all__ = ["__version__", "load_cuda_core", "make", "make_vec", "synthrom", "abi", "Button", "encode_action",
+           "COMPLEX_MOVEMENT", "COMPLEX_MOVEMENT_MASKS", "MARIO_MOVEMENT", "MARIO_MOVEMENT_MASKS", "RIGHT_ONLY",
+           "RIGHT_ONLY_MASKS", "SIMPLE_MOVEMENT", "SIMPLE_MOVEMENT_MASKS", "SIMPLE_MOVEMENT_WITH_START",
+           "SIMPLE_MOVEMENT_WITH_START_MASKS"]
 
 
 def load_cuda_core():
@@ -26,6 +45,13 @@ def load_cuda_core():
     from . import _cuda_core  # type: ignore[attr-defined]
 
     return _cuda_core
+
+
+def make(*args, **kwargs):
+    """``NesleEnv(*args, **kwargs)`` (the reference's ``nesle.make``)."""
+    from .env import NesleEnv
+
+    return NesleEnv(*args, **kwargs)
 
 
 def make_vec(*args, **kwargs):
