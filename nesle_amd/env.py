@@ -210,6 +210,7 @@ class NesleVecEnv(_VecEnvBase):
         self._cuda_step_count = 0
         self._cuda_env_step_counts = np.zeros(num_envs, dtype=np.int64)
         self._cuda_batch = self._make_batch(rom, snapshots, levels)
+        self._ram_device = None   # torch view of the batch's RAM observation (imported on first use)
         self._backends: list[Any] = []
 
     def _make_batch(self, rom: bytes, snapshots: list[bytes] | None, levels: np.ndarray | None):
@@ -227,6 +228,19 @@ class NesleVecEnv(_VecEnvBase):
         base = {"backend": BACKEND_NAME, "observation_mode": self.observation_mode, **extra}
         copy = base.copy
         return [copy() for _ in range(self.num_envs)]
+
+    def _ram_rows(self, dones: np.ndarray) -> np.ndarray:
+        """The current RAM of the ``dones`` consoles, copied to the host alone
+        (a gather on the device through the DLPack view, instead of the whole
+        [N, 2048] observation)."""
+        try:
+            import torch
+        except ImportError:  # pragma: no cover - torch is part of the image
+            return np.asarray(self._cuda_batch.ram(), dtype=np.uint8)[dones]
+        if self._ram_device is None:
+            self._ram_device = torch.from_dlpack(self._cuda_batch.ram_device())
+        idx = torch.from_numpy(np.nonzero(dones)[0]).to(self._ram_device.device)
+        return self._ram_device.index_select(0, idx).cpu().numpy()
 
     def _masks_for(self, actions: Iterable[int]) -> np.ndarray:
         a = np.asarray(actions, dtype=np.int64).ravel()
@@ -317,8 +331,7 @@ class NesleVecEnv(_VecEnvBase):
             # The returned observation of a done env is the first of its new episode.
             self._finish_episodes(dones, truncated, observations, infos)
             if self.observation_mode == "ram":
-                fresh = np.asarray(self._cuda_batch.ram(), dtype=np.uint8)
-                observations[dones] = fresh[dones]
+                observations[dones] = self._ram_rows(dones)
             else:
                 fresh = np.asarray(self._cuda_batch.render(), dtype=np.uint8)
                 self._cuda_observations = fresh
