@@ -23,19 +23,28 @@ reference's measurement harness shape), synchronize.  Inputs (ROM, snapshots,
 the whole action table) are resident in HBM before timing starts.
 
 Roofline: the step kernel's launches are timed with HIP events on the stream
-it runs on.  ``roofline`` prices the algorithmic HBM bytes per env-step
-(RAM read+write 4,096 + OAM read+write 512 + registers/PPU/reward scalars 128
-+ action 1 + reward/done 5 = 4,742 B) against 8 TB/s; its ``traffic`` is the
-HBM bytes per launch that rocprofv3 measured (FETCH_SIZE and WRITE_SIZE,
-scaled by a copy-kernel calibration) in profiles/step_kernel_65536_fs4.md.
-``roofline_valu`` gives the emulated 6502 instruction rate and the VALU pipe
-busy fraction from the same profile (SQ_INSTS_VALU x 4 cycles over 1,024
-SIMDs and the kernel time).  ``by_size`` repeats these figures, with NES
-frames/s, for 4,096 and 65,536 consoles.
+it runs on.  The binding roof is integer VALU issue: ``roofline`` divides the
+VALU lane-ops of one launch (SQ_THREAD_CYCLES_VALU, rocprofv3, committed in
+profiles/step_kernel_65536_fs4.md) by the live kernel time and prices them
+against 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz = 39.3e12 lane-ops/s; its
+``traffic`` is the HBM bytes per launch from the same summary (FETCH_SIZE and
+WRITE_SIZE, scaled by a copy-kernel calibration).  ``roofline_hbm`` prices
+the algorithmic HBM bytes per env-step (RAM read+write 4,096 + OAM
+read+write 512 + registers/PPU/reward scalars 128 + action 1 + reward/done 5
+= 4,742 B) against 8 TB/s.  ``by_size`` repeats the figures, with NES
+frames/s and the useful-lane fraction, for 4,096 and 65,536 consoles.
+
+Resets while timed: each console's first episode starts at a seeded point of
+its level's done countdown, so the timed window holds the steady auto-reset
+rate; the dones of the timed steps are summed on the device and reported.
+``reset_burst_65536`` times single steps in which a whole level, or every
+console, auto-resets, against quiet steps.
 
 ``cpu_baseline``: the reference's own CPU core (``nesle::Console`` compiled
-from the reference sources into oracle/_ref) on the host's cores, one console
-per std::thread slice, on a bounded sample of the same ROM and pad streams.
+from the reference sources into oracle/_ref) on the host's cores (the job's
+CPU share), consoles split statically over std::threads, on a bounded sample
+of the same workload: the first consoles of the 65,536 from their snapshots,
+staggered done bytes, pad streams and auto-reset.
 """
 
 from __future__ import annotations
@@ -57,6 +66,7 @@ from nesle_amd import synthrom  # noqa: E402
 ROM_SEED = 2026
 ACTION_SEED = 0x5EED
 SNAPSHOT_SEED = 77
+STAGGER_SEED = 78
 NUM_LEVELS = 8
 TIME_PENALTY = 0.01
 B_STEP = 4742                       # algorithmic HBM bytes per env-step
@@ -87,6 +97,8 @@ def size_figures(run: dict, num_envs: int) -> dict:
     algo = num_envs * B_STEP / kernel_s / 1e9
     traffic = profile_figure("traffic_bytes_per_launch", num_envs)
     measured = traffic / kernel_s / 1e9 if traffic else None
+    lane_ops = profile_figure("valu_lane_ops_per_launch", num_envs)
+    lanes = consoles_per_wave(num_envs)
     return {
         "num_envs": num_envs,
         "env_steps_per_s": run["env_steps_per_s"],
@@ -98,7 +110,22 @@ def size_figures(run: dict, num_envs: int) -> dict:
         "hbm_measured_gbs": measured,
         "hbm_measured_frac": measured / HBM_PEAK_GBS if measured else None,
         "valu_busy_frac": profile_figure("valu_busy", num_envs),
+        "valu_lane_ops_frac": lane_ops / kernel_s / VALU_PEAK_LANE_OPS if lane_ops else None,
+        "consoles_per_wave": lanes,
+        # Lanes without a console run the datapath on a dummy block: only
+        # lanes/64 of the VALU lane-ops serve a console.
+        "useful_lane_frac": lanes / 64,
+        "useful_valu_lane_ops_frac": lane_ops / kernel_s / VALU_PEAK_LANE_OPS * lanes / 64 if lane_ops else None,
     }
+
+
+def consoles_per_wave(num_envs: int) -> int:
+    """Consoles per wave64 of the step kernel's launch: the smallest power of
+    two L (at most 64) with 1,024 waves x L >= num_envs (one wave per SIMD)."""
+    lanes = 1
+    while lanes < 64 and 1024 * lanes < num_envs:
+        lanes *= 2
+    return lanes
 
 
 def log(msg: str) -> None:
@@ -130,38 +157,56 @@ def make_snapshots(core, rom: bytes, rng: np.random.Generator) -> tuple[list[byt
     return blobs, warm, done_vals
 
 
+def staggered_done(levels: np.ndarray, done_vals: list[int]) -> np.ndarray:
+    """Each console's first episode starts at a seeded point of its level's
+    countdown: done byte uniform in [1, the level's full count].  Consoles of
+    a level then finish at different steps, and any window of steps holds the
+    workload's steady reset rate (after a reset a console restarts from its
+    level's full count)."""
+    full = np.asarray(done_vals, dtype=np.int64)[levels]
+    u = np.random.default_rng(STAGGER_SEED).random(levels.size)
+    return (1 + np.floor(u * full)).astype(np.uint8)
+
+
+def reward_spec() -> dict:
+    return {"kind": "x_delta", "x_lo": synthrom.X_LO, "x_hi": synthrom.X_HI,
+            "done_addr": synthrom.DONE_BYTE, "clip": 15, "time_penalty": TIME_PENALTY}
+
+
 def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots: list[bytes] | None,
-            levels: np.ndarray | None, gray84: bool = False) -> dict:
+            levels: np.ndarray | None, gray84: bool = False, done_init: np.ndarray | None = None) -> dict:
     import torch
 
-    reward = {"kind": "x_delta", "x_lo": synthrom.X_LO, "x_hi": synthrom.X_HI,
-              "done_addr": synthrom.DONE_BYTE, "clip": 15, "time_penalty": TIME_PENALTY}
     if snapshots is not None:
-        batch = core.CudaBatch(num_envs, 4, rom, snapshots, levels, reward=reward)
+        batch = core.CudaBatch(num_envs, 4, rom, snapshots, levels, reward=reward_spec())
+        if done_init is not None:
+            batch.poke_ram_envs(synthrom.DONE_BYTE, done_init)
     else:
-        batch = core.CudaBatch(num_envs, 4, rom, reward=reward)
+        batch = core.CudaBatch(num_envs, 4, rom, reward=reward_spec())
     batch.set_stream(torch.cuda.current_stream().cuda_stream)
     auto_reset = snapshots is not None
     table = torch.from_numpy(synthrom.action_table(ACTION_SEED, num_envs, warmup + steps)).cuda()
+    # Dones of the timed steps, summed on the device (one elementwise add per step).
+    dones = torch.from_dlpack(batch.last_done_device())
+    done_count = torch.zeros(num_envs, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     for k in range(warmup):
-        out = batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
+        batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
         if gray84:
             batch.render_frames_device(rgb=False, palette=False, gray84=True)
     torch.cuda.synchronize()
     batch.set_timing(True)
-    done_total = 0
     t0 = time.perf_counter()
     for k in range(warmup, warmup + steps):
-        out = batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
+        batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
+        done_count.add_(dones)
         if gray84:
             batch.render_frames_device(rgb=False, palette=False, gray84=True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernel_ms, launches = batch.kernel_timing()
     batch.set_timing(False)
-    dones = torch.from_dlpack(out["dones"]).to(torch.int64).sum().item()
-    done_total += int(dones)
+    done_total = int(done_count.sum().item())
     # Exact emulated instruction count per env-step from one stats step.
     stats = batch.step_stats(synthrom.action_masks(ACTION_SEED, num_envs, warmup + steps))
     instr = np.asarray(stats["instructions"], dtype=np.float64)
@@ -174,8 +219,61 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
         "kernel_ms_per_launch": kernel_ms / max(launches, 1),
         "kernel_launches": launches,
         "instructions_per_env_step": float(instr.mean()),
-        "last_step_dones": done_total,
+        "dones_in_timed_window": done_total,
+        "dones_per_step": done_total / steps,
     }
+
+
+def run_reset_burst(core, rom: bytes, snapshots: list[bytes], levels: np.ndarray, done_vals: list[int],
+                    steps: int = 6) -> dict:
+    """Kernel time of single steps (HIP events, one step per timing window)
+    at 65,536 consoles: quiet steps (no console done), a burst step in which
+    every console of level 0 (1/8 of the batch) auto-resets, and one in which
+    every console does.  The ROM decrements the done byte in the NMI of every
+    frame whose incremented frame counter is a multiple of 8, so poking the
+    frame counter to 7 and the done byte to 1 makes the selected consoles
+    done in the first frame of the next step (the others get 200)."""
+    import torch
+
+    n = levels.size
+    batch = core.CudaBatch(n, 4, rom, snapshots, levels, reward=reward_spec())
+    batch.set_stream(torch.cuda.current_stream().cuda_stream)
+    table = torch.from_numpy(synthrom.action_table(ACTION_SEED, n, 3 * steps + 4)).cuda()
+    dones = torch.from_dlpack(batch.last_done_device())
+    k = 0
+
+    def timed_step() -> tuple[float, int]:
+        nonlocal k
+        batch.set_timing(True)
+        batch.step_device(table[k], auto_reset=True, synchronize=False)
+        torch.cuda.synchronize()
+        ms, _ = batch.kernel_timing()
+        batch.set_timing(False)
+        k += 1
+        return ms, int(dones.to(torch.int64).sum().item())
+
+    for _ in range(2):
+        timed_step()
+    quiet = [timed_step() for _ in range(steps)]
+    assert all(d == 0 for _, d in quiet), "quiet steps ended episodes"
+    out = {"num_envs": n, "quiet_ms": [m for m, _ in quiet]}
+    for name, sel in (("level0", levels == 0), ("all", np.ones(n, dtype=bool))):
+        vals = np.full(n, 200, dtype=np.uint8)
+        vals[sel] = 1
+        batch.poke_ram(synthrom.FRAME_COUNTER, 7)
+        batch.poke_ram_envs(synthrom.DONE_BYTE, vals)
+        ms, d = timed_step()
+        assert d == int(sel.sum()), f"burst {name}: {d} dones, expected {int(sel.sum())}"
+        after, d2 = timed_step()
+        assert d2 == 0, f"step after burst {name} ended episodes"
+        out[f"burst_{name}_ms"] = ms
+        out[f"burst_{name}_dones"] = d
+        out[f"after_burst_{name}_ms"] = after
+    q = float(np.median(out["quiet_ms"]))
+    out["quiet_median_ms"] = q
+    out["burst_level0_over_quiet"] = out["burst_level0_ms"] / q
+    out["burst_all_over_quiet"] = out["burst_all_ms"] / q
+    return out
 
 
 def run_vec_env(rom: bytes, steps: int) -> dict:
@@ -231,31 +329,56 @@ def run_ppo(rom: bytes, snapshots: list[bytes], updates: int) -> dict:
     }
 
 
-def cpu_baseline(rom: bytes, target_seconds: float) -> dict | None:
+def cpu_share() -> tuple[int, dict]:
+    """Threads for the CPU baseline: every CPU this process may run on, unless
+    the host grants the job a smaller CPU share through OMP_NUM_THREADS (a
+    one-GPU box gives one GPU's job 16 CPUs; threads beyond the share only
+    time-slice).  Returns the count and what it was derived from."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        affinity = nproc
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    threads = affinity
+    if share.isdigit() and 0 < int(share) < affinity:
+        threads = int(share)
+    return threads, {"nproc": nproc, "affinity": affinity, "omp_num_threads": share or None}
+
+
+def cpu_baseline(rom: bytes, snaps: list[bytes], levels: np.ndarray, done_init: np.ndarray,
+                 target_seconds: float) -> dict | None:
+    """The reference's CPU core on the benchmark's own workload: the first
+    consoles of the 65,536 (same snapshot levels, staggered done bytes, pad
+    streams), auto-reset from the level's snapshot whenever the done byte
+    reaches 0, consoles split statically over std::threads."""
     try:
         from oracle import oracle as O
     except Exception as exc:  # pragma: no cover
         log(f"cpu baseline unavailable: {exc}")
         return None
     kind = "reference" if O.ref_available() else "port"
-    threads = max(1, min(16, O.cpu_threads()))
+    threads, share = cpu_share()
+    envs = 8 * threads
+    lv, di = levels[:envs], done_init[:envs]
     # Calibrate on a short run, then size the sample to ~target_seconds.
-    envs, steps = threads, 20
-    secs, _, _ = O.run_batch(rom, envs, steps, 4, ACTION_SEED, threads, kind=kind)
-    rate = envs * steps / secs
-    steps = max(50, int(target_seconds * rate / envs))
-    secs, checksum, instr = O.run_batch(rom, envs, steps, 4, ACTION_SEED, threads, kind=kind)
+    secs, _, _, _ = O.run_levels(rom, snaps, lv, di, synthrom.DONE_BYTE, 10, 4, ACTION_SEED, 0, threads, kind=kind)
+    steps = max(50, int(target_seconds * envs * 10 / secs / envs))
+    secs, _, instr, resets = O.run_levels(rom, snaps, lv, di, synthrom.DONE_BYTE, steps, 4, ACTION_SEED, 0,
+                                          threads, kind=kind)
     value = envs * steps / secs
     return {
         "value": value,
         "unit": "env-steps/s",
         "cores": threads,
         "kind": kind,
-        "sample": f"{envs} consoles x {steps} env-steps (frame-skip 4) from power-on, same ROM and pad "
+        "sample": f"consoles 0-{envs - 1} of the 65,536-console workload x {steps} env-steps (frame-skip 4) from "
+                  f"their snapshots with the staggered done bytes, auto-reset on done ({resets} resets), same pad "
                   f"streams, {threads} std::threads, {secs:.1f} s",
         "per_core": value / threads,
         "instructions_per_env_step": instr / (envs * steps),
         "cpu_model": _cpu_model(),
+        **share,
     }
 
 
@@ -299,6 +422,8 @@ def main() -> int:
     ap.add_argument("--ppo-updates", type=int, default=2,
                     help="PPO updates of 8,192 consoles x 128 steps (the first warms up; 0 skips)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-burst", dest="burst", action="store_false",
+                    help="skip the single-step reset-burst timings")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (scales rocprof FETCH_SIZE/WRITE_SIZE)")
@@ -323,10 +448,18 @@ def main() -> int:
     log("capturing snapshot bank")
     snaps, warm, done_vals = make_snapshots(core, rom, rng)
     levels = rng.integers(0, NUM_LEVELS, args.envs).astype(np.uint8)
+    done_init = staggered_done(levels, done_vals)
 
     log(f"timing {args.envs} envs x {args.steps} steps (warmup {args.warmup})")
-    big = run_gpu(core, rom, args.envs, args.steps, args.warmup, snaps, levels)
-    log(f"  {big['env_steps_per_s']:.0f} env-steps/s, kernel {big['kernel_ms_per_launch']:.2f} ms/launch")
+    big = run_gpu(core, rom, args.envs, args.steps, args.warmup, snaps, levels, done_init=done_init)
+    log(f"  {big['env_steps_per_s']:.0f} env-steps/s, kernel {big['kernel_ms_per_launch']:.2f} ms/launch, "
+        f"{big['dones_in_timed_window']} auto-resets while timed")
+    burst = None
+    if args.burst:
+        log("reset bursts: single-step kernel times")
+        burst = run_reset_burst(core, rom, snaps, levels, done_vals)
+        log(f"  quiet {burst['quiet_median_ms']:.2f} ms, level burst {burst['burst_level0_ms']:.2f} ms, "
+            f"all {burst['burst_all_ms']:.2f} ms")
     log(f"timing {args.small_envs} envs x {args.small_steps} steps (no resets)")
     small = run_gpu(core, rom, args.small_envs, args.small_steps, max(5, args.warmup // 4), None, None)
     log(f"  {small['env_steps_per_s']:.0f} env-steps/s")
@@ -350,6 +483,8 @@ def main() -> int:
     kernel_s = big["kernel_ms_per_launch"] / 1000.0
     hbm_achieved = args.envs * B_STEP / kernel_s / 1e9
     instr_rate = big["instructions_per_env_step"] * args.envs / kernel_s
+    lane_ops = profile_figure("valu_lane_ops_per_launch", args.envs)
+    valu_achieved = lane_ops / kernel_s / 1e12 if lane_ops else None
     result = {
         "metric": "env-steps/s (frameskip 4)",
         "value": big["env_steps_per_s"],
@@ -373,30 +508,37 @@ def main() -> int:
         },
         "nes_frames_per_s": 4 * big["env_steps_per_s"],
         "roofline": {
-            "bound": "hbm",
+            "bound": "valu",
+            "achieved": valu_achieved,
+            "peak": VALU_PEAK_LANE_OPS / 1e12,
+            "unit": "T int32 lane-ops/s",
+            "frac": valu_achieved * 1e12 / VALU_PEAK_LANE_OPS if valu_achieved else None,
+            "traffic": profile_figure("traffic_bytes_per_launch", args.envs),
+            "source": "achieved = SQ_THREAD_CYCLES_VALU per launch (= SQ_INSTS_VALU x 64 x VALU utilisation, "
+                      "rocprofv3, profiles/step_kernel_65536_fs4.md) / step-kernel time per launch (HIP events, "
+                      "this run); peak = 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz; traffic = HBM bytes per launch "
+                      "(FETCH_SIZE x2.000 + WRITE_SIZE x1.000, same summary)",
+            "kernel_ms_per_launch": big["kernel_ms_per_launch"],
+            "emulated_instr_per_s": instr_rate,
+            "instructions_per_env_step": big["instructions_per_env_step"],
+            "valu_busy_frac": profile_figure("valu_busy", args.envs),
+        },
+        "roofline_hbm": {
             "achieved": hbm_achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": hbm_achieved / HBM_PEAK_GBS,
-            "traffic": profile_figure("traffic_bytes_per_launch", args.envs),
-            "traffic_source": "rocprofv3 FETCH_SIZE x2.000 + WRITE_SIZE x1.000, profiles/step_kernel_65536_fs4.md",
-        },
-        "roofline_valu": {
-            "achieved_emulated_instr_per_s": instr_rate,
-            "instructions_per_env_step": big["instructions_per_env_step"],
-            "valu_busy_frac": profile_figure("valu_busy", args.envs),
-            "valu_busy_source": "rocprofv3 SQ_INSTS_VALU x 4 cycles / (1,024 SIMDs x kernel time), "
-                                "profiles/step_kernel_65536_fs4.md",
-            "peak_int32_lane_ops_per_s": VALU_PEAK_LANE_OPS,
-            "kernel_ms_per_launch": big["kernel_ms_per_launch"],
+            "algorithmic_bytes_per_env_step": B_STEP,
+            "measured_bytes_per_env_step": (profile_figure("traffic_bytes_per_launch", args.envs) or 0) / args.envs
+            or None,
         },
         "by_size": [size_figures(small, args.small_envs), size_figures(big, args.envs)],
         "extra": {"envs_4096": small, "envs_65536": big, "pixels_16384_gray84": pixel, "ppo_8192x128": ppo,
-                  "vec_env_ram_4096": vec},
+                  "vec_env_ram_4096": vec, "reset_burst_65536": burst},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(rom, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(rom, snaps, levels, done_init, args.cpu_seconds)
     print(json.dumps(result))
     return 0
 

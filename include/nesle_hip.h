@@ -190,6 +190,14 @@ int nesle_set_env_levels(nesle_batch* b, const uint8_t* env_to_level);
 /* Write one RAM byte in every console.  Replaces poke_ram (cuda_module.cu:939-946). */
 int nesle_poke_ram(nesle_batch* b, uint32_t address, uint32_t value);
 
+/* Write one RAM byte per console: values[env] (num_envs bytes, host or
+ * device) into RAM[address & 0x7FF] of console env.  Reward baselines are
+ * left as they are.  The per-console form of poke_ram (cuda_module.cu:939-946),
+ * which writes one value into every console; no reference counterpart
+ * otherwise.  Used to stagger episode counters across consoles.  With device
+ * values the call only enqueues work on the batch's stream. */
+int nesle_poke_ram_envs(nesle_batch* b, uint32_t address, const uint8_t* values, int on_device);
+
 int nesle_synchronize(nesle_batch* b);
 int nesle_set_stream(nesle_batch* b, void* hip_stream);
 

@@ -122,6 +122,7 @@ def lib():
         "nesle_snapshot_export": (ctypes.c_int, [vp, ctypes.c_uint32, _U8P]),
         "nesle_set_env_levels": (ctypes.c_int, [vp, _U8P]),
         "nesle_poke_ram": (ctypes.c_int, [vp, ctypes.c_uint32, ctypes.c_uint32]),
+        "nesle_poke_ram_envs": (ctypes.c_int, [vp, ctypes.c_uint32, vp, ctypes.c_int]),
         "nesle_synchronize": (ctypes.c_int, [vp]),
         "nesle_set_stream": (ctypes.c_int, [vp, vp]),
         "nesle_num_envs": (ctypes.c_uint32, [vp]),
@@ -275,6 +276,12 @@ class Batch:
 
     def poke_ram(self, address: int, value: int) -> None:
         _check(lib().nesle_poke_ram(self.h, address, value))
+
+    def poke_ram_envs(self, address: int, values: np.ndarray) -> None:
+        """RAM[address] of console e = values[e] (host uint8, one per console)."""
+        v = np.ascontiguousarray(values, dtype=np.uint8)
+        assert v.shape == (self.n,)
+        _check(lib().nesle_poke_ram_envs(self.h, address, v.ctypes.data, 0))
 
     def synchronize(self) -> None:
         _check(lib().nesle_synchronize(self.h))

@@ -374,6 +374,14 @@ public:
 
     void poke_ram(std::uint16_t address, std::uint8_t value) { check(nesle_poke_ram(h_, address, value)); }
 
+    // One RAM byte per console (host uint8 array of shape (num_envs,)).
+    void poke_ram_envs(std::uint16_t address, const py::array_t<std::uint8_t, py::array::c_style | py::array::forcecast>& values) {
+        const auto v = values.request();
+        if (v.ndim != 1 || static_cast<std::uint32_t>(v.shape[0]) != n_)
+            throw py::value_error("values must have shape (num_envs,)");
+        check(nesle_poke_ram_envs(h_, address, static_cast<const std::uint8_t*>(v.ptr), 0));
+    }
+
     py::bytes save_state(std::uint32_t env) const {
         std::string out(NESLE_STATE_BYTES, '\0');
         check(nesle_save_state(h_, env, reinterpret_cast<std::uint8_t*>(out.data())));
@@ -595,6 +603,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("reset_envs", &CudaBatch::reset_envs, py::arg("mask"))
         .def("reset_envs_device", &CudaBatch::reset_envs_device, py::arg("mask"))
         .def("poke_ram", &CudaBatch::poke_ram, py::arg("address"), py::arg("value"))
+        .def("poke_ram_envs", &CudaBatch::poke_ram_envs, py::arg("address"), py::arg("values"))
         .def("save_state", &CudaBatch::save_state, py::arg("env"))
         .def("load_state", &CudaBatch::load_state, py::arg("state"), py::arg("mask") = py::none())
         .def("snapshot_capture", &CudaBatch::snapshot_capture, py::arg("env"), py::arg("slot"))

@@ -764,6 +764,21 @@ int nesle_poke_ram(nesle_batch* b, std::uint32_t address, std::uint32_t value) {
     });
 }
 
+int nesle_poke_ram_envs(nesle_batch* b, std::uint32_t address, const std::uint8_t* values, int on_device) {
+    return guarded([&] {
+        if (b == nullptr || values == nullptr) throw InvalidArgument("null argument");
+        b->activate();
+        const std::uint8_t* dv = values;
+        if (!on_device) {
+            b->host_to_device(b->d_mask, values, b->n(), "copy RAM values");
+            dv = b->d_mask;
+        }
+        hip_check(nesle::launch_poke_ram_envs(b->ds, address, dv, b->stream), "poke_ram_envs_kernel");
+        b->refresh_obs();
+        if (!on_device) b->sync();   // the staging buffer is reused by the next call
+    });
+}
+
 int nesle_synchronize(nesle_batch* b) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");

@@ -117,6 +117,12 @@ __global__ void __launch_bounds__(kBlock) poke_ram_kernel(DeviceState s, std::ui
     if (env < s.n) s.ram[static_cast<std::size_t>(addr & 0x7FF) * s.pitch + env] = static_cast<std::uint8_t>(value);
 }
 
+__global__ void __launch_bounds__(kBlock) poke_ram_envs_kernel(DeviceState s, std::uint32_t addr,
+                                                               const std::uint8_t* values) {
+    const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
+    if (env < s.n) s.ram[static_cast<std::size_t>(addr & 0x7FF) * s.pitch + env] = values[env];
+}
+
 __global__ void __launch_bounds__(kBlock) seed_kernel(DeviceState s) {
     const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
     if (env < s.n) seed_baselines(s, env);
@@ -180,6 +186,12 @@ hipError_t launch_actions_i64(std::uint8_t* dst, const long long* src, std::uint
 
 hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32_t value, hipStream_t stream) {
     poke_ram_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, addr, value);
+    return hipGetLastError();
+}
+
+hipError_t launch_poke_ram_envs(const DeviceState& s, std::uint32_t addr, const std::uint8_t* values,
+                                hipStream_t stream) {
+    poke_ram_envs_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, addr, values);
     return hipGetLastError();
 }
 

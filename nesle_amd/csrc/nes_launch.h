@@ -22,6 +22,9 @@ hipError_t launch_save_blob(const DeviceState& s, std::uint32_t env, std::uint8_
 hipError_t launch_ram_obs(const DeviceState& s, std::uint8_t* obs, hipStream_t stream);
 hipError_t launch_actions_i64(std::uint8_t* dst, const long long* src, std::uint32_t n, hipStream_t stream);
 hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32_t value, hipStream_t stream);
+// One RAM byte per console: values[env] (device, n bytes) into RAM[addr].
+hipError_t launch_poke_ram_envs(const DeviceState& s, std::uint32_t addr, const std::uint8_t* values,
+                                hipStream_t stream);
 hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
 // Presentation snapshot (and pre-render latch) from live state, masked.
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);

@@ -1,35 +1,40 @@
-"""SB3-style vector environment and single Gymnasium-style environment over the
-HIP batch: the drop-in for the reference's ``nesle.env`` CUDA backend
-(src/nesle/env.py:365-818 ``NesleVecEnv``, 821-905 ``NesleEnv``,
-src/nesle/__init__.py:58-61 ``make_vec``).
+"""Stable-Baselines3 / Gymnasium environments over the HIP console batch: the
+drop-in for the CUDA backend of the reference's ``nesle.env``
+(src/nesle/env.py: ``NesleVecEnv``, ``NesleEnv``; src/nesle/__init__.py
+``make_vec``).
 
-Semantics kept from the reference's CUDA branch (env.py:549-741):
+The contract, as the reference's tests state it
+(tests/test_critical_fixes.py:59-196, tests/test_env_reset_state.py):
 
-* observations are the RAM (``observation_mode="ram"``, [N, 2048]) or RGB
-  frames ([N, 240, 256, 3]) copied to host NumPy arrays; RGB frames can be
-  copied every ``observation_cadence``-th step only (stale in between);
-* rewards/dones come from the batch's in-kernel reward rule; with
-  ``max_episode_steps`` an episode is also cut (``truncated``) after that
-  many steps;
-* SB3's auto-reset contract: a done env's info carries
-  ``terminal_observation`` (the last observation of the episode),
-  ``terminated`` and ``truncated``; the env is reset (snapshot level or
-  power-on) and the returned observation is the first one of the new
-  episode; ``reset_infos`` is refreshed;
-* ``reset_state_path(s)`` load FCEUX FCS states (gzip-wrapped ``.state``
-  files are unpacked) or canonical state blobs; several states are assigned
-  round-robin unless ``env_to_level`` says otherwise.
+* ``reset()`` returns the observations of every console after a reset:
+  RAM rows ``[N, 2048]`` (``observation_mode="ram"``) or RGB frames
+  ``[N, 240, 256, 3]``, host NumPy arrays;
+* ``step(actions)`` takes one action index per console (into the chosen
+  action table) and returns ``(observations, rewards, dones, infos)``; a
+  console whose episode ended (the batch's reward rule says done, or it ran
+  ``max_episode_steps`` steps) is reset before ``step`` returns: its
+  observation is the first of the new episode and its info holds
+  ``terminal_observation`` (the last observation of the old one),
+  ``terminated`` and ``truncated`` (a step-limit cut is a truncation even if
+  the rule also said done); ``reset_infos`` is refreshed for it;
+* RGB observations can be copied every ``observation_cadence``-th step
+  only; in between the previous copy is returned and marked stale;
+* ``step_reward(actions)`` is the same step without observation copies;
+* several reset states are spread over the consoles round-robin unless
+  ``env_to_level`` names each console's state; a console resets to its own.
 
-Only the HIP backend exists here: the reference's CPU "synthetic" and
-"native" backends are not provided (``backend`` must be "auto" or "cuda").
-Per-env Python loops of the reference (action-mask mapping, terminal
-observation copies) are NumPy operations.
+Design here: the batch (``nesle_amd._cuda_core.CudaBatch``) does the
+emulation and the resets on the device; this module keeps three small
+host-side pieces — the action table lookup, an episode clock per console
+(``_EpisodeClock``) and an observation reader (``_Observer``) that knows
+which copy each mode needs — and builds the SB3 return values from whole
+arrays (no per-console Python work except the info dicts SB3 requires).
+Only the HIP backend exists (``backend`` "auto" or "cuda").
 """
 
 from __future__ import annotations
 
 import gzip
-from dataclasses import dataclass
 from pathlib import Path
 from typing import Any, Iterable, Sequence
 
@@ -39,10 +44,10 @@ from nesle_amd import actions as _actions
 
 try:
     import gymnasium as gym
-    from gymnasium import spaces
+    from gymnasium import spaces as _gym_spaces
 except ImportError:  # gymnasium is optional
     gym = None
-    spaces = None
+    _gym_spaces = None
 
 try:
     from stable_baselines3.common.vec_env import VecEnv as _SB3VecEnv
@@ -51,98 +56,174 @@ except ImportError:  # stable-baselines3 is optional
 
 CPU_RAM_BYTES = 2048
 FRAME_SHAPE = (240, 256, 3)
-RAM_SHAPE = (CPU_RAM_BYTES,)
-FRAME_DTYPE = np.uint8
 BACKEND_NAME = "cuda-console"
+GZIP_MAGIC = b"\x1f\x8b"
+
+# Accepted spellings of the two observation modes (lower case, '-' as '_').
+_MODE_ALIASES = {"rgb": "rgb_array", "rgb_array": "rgb_array", "frame": "rgb_array",
+                 "ram": "ram", "cpu_ram": "ram"}
 
 
-class DiscreteSpace:
-    """Stand-in for gymnasium.spaces.Discrete when gymnasium is absent."""
-
-    def __init__(self, n: int) -> None:
-        self.n = int(n)
-        self.shape = ()
-        self.dtype = np.int64
-
-    def sample(self) -> int:
-        return int(np.random.default_rng().integers(self.n))
-
-    def contains(self, value: Any) -> bool:
-        try:
-            item = int(value)
-        except (TypeError, ValueError):
-            return False
-        return 0 <= item < self.n
+def observation_mode_of(name: str) -> str:
+    """Canonical observation mode ("rgb_array" or "ram") for an accepted name."""
+    mode = _MODE_ALIASES.get(str(name).lower().replace("-", "_"))
+    if mode is None:
+        raise ValueError("observation_mode must be 'rgb_array' or 'ram'")
+    return mode
 
 
-class BoxSpace:
-    """Stand-in for gymnasium.spaces.Box when gymnasium is absent."""
-
-    def __init__(self, low: int, high: int, shape: tuple[int, ...], dtype: Any) -> None:
-        self.low, self.high, self.shape, self.dtype = low, high, shape, np.dtype(dtype)
-
-    def sample(self) -> np.ndarray:
-        return np.random.default_rng().integers(self.low, self.high + 1, size=self.shape, dtype=self.dtype)
-
-    def contains(self, value: Any) -> bool:
-        a = np.asarray(value)
-        return a.shape == self.shape and a.dtype == self.dtype
+def read_state_file(path: str | Path) -> bytes:
+    """Bytes of a reset-state file; Gym/Stable Retro ``.state`` files are
+    gzip streams and come back unpacked."""
+    data = Path(path).read_bytes()
+    if data.startswith(GZIP_MAGIC):
+        data = gzip.decompress(data)
+    return data
 
 
-def _box(low: int, high: int, shape: tuple[int, ...], dtype: Any) -> Any:
-    return spaces.Box(low, high, shape=shape, dtype=dtype) if spaces is not None else BoxSpace(low, high, shape, dtype)
-
-
-def _discrete(n: int) -> Any:
-    return spaces.Discrete(n) if spaces is not None else DiscreteSpace(n)
-
-
-def _normalize_observation_mode(observation_mode: str) -> str:
-    key = observation_mode.lower().replace("-", "_")
-    if key in {"rgb", "rgb_array", "frame"}:
-        return "rgb_array"
-    if key in {"ram", "cpu_ram"}:
-        return "ram"
-    raise ValueError("observation_mode must be 'rgb_array' or 'ram'")
-
-
-def _load_reset_state(path: str | Path) -> bytes:
-    """A reset state file; gzip-wrapped Stable Retro / Gym Retro ``.state`` files are unpacked."""
-    raw = Path(path).read_bytes()
-    return gzip.decompress(raw) if raw[:2] == b"\x1f\x8b" else raw
-
-
-def _resolve_reset_state_paths(reset_state_path, reset_state_paths) -> list[Path] | None:
-    if reset_state_path is not None and reset_state_paths is not None:
+def state_file_list(reset_state_path, reset_state_paths) -> list[Path]:
+    """The reset-state files asked for (empty: power-on resets)."""
+    given = [x for x in (reset_state_path, reset_state_paths) if x is not None]
+    if len(given) == 2:
         raise ValueError("Pass exactly one of reset_state_path or reset_state_paths, not both")
-    if reset_state_paths is not None:
-        if len(reset_state_paths) == 0:
-            raise ValueError("reset_state_paths must contain at least one path")
-        return [Path(p) for p in reset_state_paths]
+    if reset_state_paths is not None and len(reset_state_paths) == 0:
+        raise ValueError("reset_state_paths must contain at least one path")
     if reset_state_path is not None:
         return [Path(reset_state_path)]
-    return None
+    return [Path(p) for p in (reset_state_paths or ())]
 
 
-@dataclass(frozen=True)
-class BackendConfig:
-    rom_path: str
-    num_envs: int
-    frameskip: int = 4
-    action_space: str | Sequence[int] = "simple"
-    device: str = "auto"
-    backend: str = "auto"
-    observation_mode: str = "rgb_array"
-    observation_cadence: int = 1
-    max_episode_steps: int = 0
-    reset_state_path: str | None = None
+def level_map(num_states: int, num_envs: int, env_to_level) -> np.ndarray | None:
+    """Per-console reset state: explicit, or round-robin over the states;
+    None when there is at most one state (every console shares it)."""
+    if num_states <= 1:
+        if env_to_level is not None:
+            raise ValueError("env_to_level requires more than one snapshot")
+        return None
+    if env_to_level is None:
+        return (np.arange(num_envs) % num_states).astype(np.uint8)
+    levels = np.asarray(env_to_level)
+    if levels.shape != (num_envs,):
+        raise ValueError(f"env_to_level shape must be ({num_envs},), got {levels.shape}")
+    if levels.size and (levels.min() < 0 or levels.max() >= num_states):
+        raise ValueError("env_to_level contains index >= number of snapshots")
+    return levels.astype(np.uint8)
+
+
+class _Discrete:
+    """Discrete(n) when gymnasium is not installed."""
+
+    def __init__(self, n: int) -> None:
+        self.n, self.shape, self.dtype = int(n), (), np.dtype(np.int64)
+
+    def sample(self) -> int:
+        return int(np.random.randint(self.n))
+
+    def contains(self, x: Any) -> bool:
+        return isinstance(x, (int, np.integer)) and 0 <= int(x) < self.n
+
+
+class _Box:
+    """Box(0, 255, shape, uint8) when gymnasium is not installed."""
+
+    def __init__(self, shape: tuple[int, ...]) -> None:
+        self.low, self.high, self.shape, self.dtype = 0, 255, tuple(shape), np.dtype(np.uint8)
+
+    def sample(self) -> np.ndarray:
+        return np.random.randint(0, 256, size=self.shape).astype(np.uint8)
+
+    def contains(self, x: Any) -> bool:
+        return isinstance(x, np.ndarray) and x.shape == self.shape and x.dtype == self.dtype
+
+
+def _spaces(obs_shape: tuple[int, ...], n_actions: int) -> tuple[Any, Any]:
+    if _gym_spaces is None:
+        return _Box(obs_shape), _Discrete(n_actions)
+    return _gym_spaces.Box(0, 255, shape=obs_shape, dtype=np.uint8), _gym_spaces.Discrete(n_actions)
+
+
+class _EpisodeClock:
+    """Steps since each console's episode began, and the optional limit."""
+
+    def __init__(self, num_envs: int, limit: int) -> None:
+        self.limit = int(limit)
+        self.steps = np.zeros(num_envs, dtype=np.int64)
+
+    def tick(self) -> np.ndarray:
+        """Advance every console by one step; returns the consoles whose
+        episode hit the limit."""
+        self.steps += 1
+        if self.limit <= 0:
+            return np.zeros(self.steps.shape, dtype=bool)
+        return self.steps >= self.limit
+
+    def restart(self, which: np.ndarray | None = None) -> None:
+        if which is None:
+            self.steps.fill(0)
+        else:
+            self.steps[which] = 0
+
+
+class _Observer:
+    """Reads the observation a mode needs from the batch.
+
+    RAM: the batch's RAM rows every step (after resets, only the reset rows
+    are fetched again, gathered on the device).  RGB: the frame copy of the
+    step on cadence steps, the previous copy otherwise."""
+
+    def __init__(self, batch, mode: str, cadence: int) -> None:
+        self.batch, self.mode, self.cadence = batch, mode, cadence
+        self.frames: np.ndarray | None = None   # last RGB copy handed out
+        self.steps = 0
+        self._ram_dev = None
+
+    def after_reset(self, frames: np.ndarray) -> np.ndarray:
+        self.steps = 0
+        self.frames = frames
+        return self.batch.ram() if self.mode == "ram" else frames
+
+    def step(self, masks: np.ndarray) -> tuple[dict, np.ndarray, dict]:
+        """One batch step; returns (step result, observations, info flags)."""
+        self.steps += 1
+        if self.mode == "ram":
+            result = self.batch.step(masks, render_frame=False, copy_obs=False)
+            return result, self.batch.ram(), {"observations_copied": True, "observations_stale": False,
+                                              "rgb_observations_copied": False}
+        fresh = self.cadence <= 1 or self.steps % self.cadence == 0
+        result = self.batch.step(masks, render_frame=fresh, copy_obs=fresh)
+        if fresh:
+            self.frames = result["obs"]
+        elif self.frames is None:
+            self.frames = self.batch.render()
+        return result, self.frames, {"observations_copied": fresh, "observations_stale": not fresh,
+                                     "rgb_observations_copied": fresh}
+
+    def current(self) -> np.ndarray:
+        """The observation of every console now (no cadence)."""
+        return self.batch.ram() if self.mode == "ram" else self.batch.render()
+
+    def replace_rows(self, obs: np.ndarray, which: np.ndarray) -> np.ndarray:
+        """``obs`` with the rows of ``which`` replaced by the current state."""
+        if self.mode == "ram":
+            obs[which] = self._ram_gather(np.flatnonzero(which))
+            return obs
+        self.frames = self.batch.render()
+        return np.where(which[:, None, None, None], self.frames, obs)
+
+    def _ram_gather(self, rows: np.ndarray) -> np.ndarray:
+        import torch
+
+        if self._ram_dev is None:
+            self._ram_dev = torch.from_dlpack(self.batch.ram_device())
+        index = torch.as_tensor(rows, dtype=torch.long).to(self._ram_dev.device)
+        return self._ram_dev.index_select(0, index).cpu().numpy()
 
 
 _VecEnvBase = _SB3VecEnv if _SB3VecEnv is not None else object
 
 
 class NesleVecEnv(_VecEnvBase):
-    """N consoles behind SB3's VecEnv ``reset``/``step`` contract."""
+    """``num_envs`` consoles behind SB3's ``VecEnv`` interface."""
 
     metadata = {"render_modes": ["rgb_array"], "render_fps": 60}
 
@@ -153,270 +234,201 @@ class NesleVecEnv(_VecEnvBase):
                  reset_state_path: str | Path | None = None,
                  reset_state_paths: Sequence[str | Path] | None = None,
                  env_to_level: Sequence[int] | np.ndarray | None = None, *, rom_bytes: bytes | None = None) -> None:
-        if num_envs <= 0:
-            raise ValueError("num_envs must be positive")
-        if frameskip <= 0:
-            raise ValueError("frameskip must be positive")
-        if observation_cadence <= 0:
-            raise ValueError("observation_cadence must be positive")
-        if render_mode not in (None, "rgb_array"):
+        # Every argument is checked before the ROM is read or the GPU touched.
+        for name, value in (("num_envs", num_envs), ("frameskip", frameskip),
+                            ("observation_cadence", observation_cadence)):
+            if value <= 0:
+                raise ValueError(f"{name} must be positive")
+        if render_mode is not None and render_mode != "rgb_array":
             raise ValueError("render_mode must be None or 'rgb_array'")
-        if backend.lower() not in ("auto", "cuda"):
+        if str(backend).lower() not in ("auto", "cuda"):
             raise ValueError(f"backend {backend!r} is not provided: this package runs the HIP console "
                              "(backend='cuda' or 'auto')")
-        observation_mode = _normalize_observation_mode(observation_mode)
-        masks = _actions.action_masks(action_space)
-        snapshots: list[bytes] | None = None
-        levels: np.ndarray | None = None
-        paths = _resolve_reset_state_paths(reset_state_path, reset_state_paths)
-        if paths is not None:
-            snapshots = [_load_reset_state(p) for p in paths]
-            if len(snapshots) > 1:
-                if env_to_level is None:
-                    levels = (np.arange(num_envs) % len(snapshots)).astype(np.uint8)
-                else:
-                    levels = np.asarray(env_to_level, dtype=np.uint8)
-                    if levels.shape != (num_envs,):
-                        raise ValueError(f"env_to_level shape must be ({num_envs},), got {levels.shape}")
-                    if int(levels.max(initial=0)) >= len(snapshots):
-                        raise ValueError("env_to_level contains index >= number of snapshots")
-            elif env_to_level is not None:
-                raise ValueError("env_to_level requires more than one snapshot")
-        rom = rom_bytes if rom_bytes is not None else Path(rom_path).read_bytes()
+        mode = observation_mode_of(observation_mode)
+        table = _actions.action_masks(action_space)
+        files = state_file_list(reset_state_path, reset_state_paths)
+        states = [read_state_file(p) for p in files]
+        levels = level_map(len(states), num_envs, env_to_level)
 
-        self.config = BackendConfig(rom_path=str(rom_path), num_envs=num_envs, frameskip=frameskip,
-                                    action_space=action_space, device=device, backend=backend,
-                                    observation_mode=observation_mode, observation_cadence=observation_cadence,
-                                    max_episode_steps=max_episode_steps,
-                                    reset_state_path=None if reset_state_path is None else str(reset_state_path))
+        self.num_envs, self.frameskip = int(num_envs), int(frameskip)
+        self.observation_mode, self.observation_cadence = mode, int(observation_cadence)
+        self.max_episode_steps = int(max_episode_steps)
         self.render_mode = render_mode
-        self.observation_mode = observation_mode
-        self.num_envs = num_envs
-        self.frameskip = frameskip
-        self.observation_cadence = observation_cadence
-        self.action_masks = masks
-        self._mask_table = np.asarray(masks, dtype=np.uint8)
-        self.action_space = _discrete(len(masks))
-        self.observation_space = _box(0, 255, RAM_SHAPE if observation_mode == "ram" else FRAME_SHAPE, np.uint8)
+        self.device, self.backend = device, backend
+        self.action_masks = tuple(table)
+        self._table = np.asarray(table, dtype=np.uint8)
+        obs_shape = (CPU_RAM_BYTES,) if mode == "ram" else FRAME_SHAPE
+        self.observation_space, self.action_space = _spaces(obs_shape, len(table))
         if _SB3VecEnv is not None:
-            _SB3VecEnv.__init__(self, num_envs, self.observation_space, self.action_space)
-        self.reset_infos: list[dict[str, Any]] = [{} for _ in range(num_envs)]
-        self.buf_infos: list[dict[str, Any]] = [{} for _ in range(num_envs)]
-        self._pending_actions: np.ndarray | None = None
-        self._seeds: list[int | None] = [None] * num_envs
-        self._options: list[dict[str, Any]] = [{} for _ in range(num_envs)]
-        self._closed = False
-        self._cuda_observations: np.ndarray | None = None
-        self._cuda_step_count = 0
-        self._cuda_env_step_counts = np.zeros(num_envs, dtype=np.int64)
-        self._cuda_batch = self._make_batch(rom, snapshots, levels)
-        self._ram_device = None   # torch view of the batch's RAM observation (imported on first use)
-        self._backends: list[Any] = []
+            _SB3VecEnv.__init__(self, self.num_envs, self.observation_space, self.action_space)
 
-    def _make_batch(self, rom: bytes, snapshots: list[bytes] | None, levels: np.ndarray | None):
-        """env.py:334-362."""
+        rom = rom_bytes if rom_bytes is not None else Path(rom_path).read_bytes()
+        self._cuda_batch = self._open_batch(rom, states, levels)
+        self._observer = _Observer(self._cuda_batch, mode, self.observation_cadence)
+        self._clock = _EpisodeClock(self.num_envs, self.max_episode_steps)
+        self._queued: np.ndarray | None = None
+        self._seeds: list[int | None] = [None] * self.num_envs
+        self._options: list[dict[str, Any]] = [{} for _ in range(self.num_envs)]
+        self.reset_infos: list[dict[str, Any]] = [self._base_info() for _ in range(self.num_envs)]
+        self.buf_infos: list[dict[str, Any]] = [{} for _ in range(self.num_envs)]
+        self.closed = False
+
+    def _open_batch(self, rom: bytes, states: list[bytes], levels: np.ndarray | None):
+        """The batch: power-on resets, one shared reset state, or one state per
+        console (the CudaBatch constructor forms of cuda_module.cu:389-467)."""
         from nesle_amd import load_cuda_core
 
         core = load_cuda_core()
-        if snapshots is None:
-            return core.CudaBatch(self.num_envs, self.frameskip, rom)
-        if len(snapshots) == 1:
-            return core.CudaBatch(self.num_envs, self.frameskip, rom, snapshots[0])
-        return core.CudaBatch(self.num_envs, self.frameskip, rom, snapshots, levels)
+        args: tuple = (self.num_envs, self.frameskip, rom)
+        if len(states) == 1:
+            args += (states[0],)
+        elif states:
+            args += (states, levels)
+        return core.CudaBatch(*args)
 
-    def _infos(self, **extra) -> list[dict[str, Any]]:
-        base = {"backend": BACKEND_NAME, "observation_mode": self.observation_mode, **extra}
-        copy = base.copy
-        return [copy() for _ in range(self.num_envs)]
+    def _base_info(self) -> dict[str, Any]:
+        return {"backend": BACKEND_NAME, "observation_mode": self.observation_mode}
 
-    def _ram_rows(self, dones: np.ndarray) -> np.ndarray:
-        """The current RAM of the ``dones`` consoles, copied to the host alone
-        (a gather on the device through the DLPack view, instead of the whole
-        [N, 2048] observation)."""
-        try:
-            import torch
-        except ImportError:  # pragma: no cover - torch is part of the image
-            return np.asarray(self._cuda_batch.ram(), dtype=np.uint8)[dones]
-        if self._ram_device is None:
-            self._ram_device = torch.from_dlpack(self._cuda_batch.ram_device())
-        idx = torch.from_numpy(np.nonzero(dones)[0]).to(self._ram_device.device)
-        return self._ram_device.index_select(0, idx).cpu().numpy()
-
-    def _masks_for(self, actions: Iterable[int]) -> np.ndarray:
-        a = np.asarray(actions, dtype=np.int64).ravel()
-        if a.shape != (self.num_envs,):
-            raise ValueError(f"expected actions with shape ({self.num_envs},), got {a.shape}")
-        if (a < 0).any() or (a >= len(self.action_masks)).any():
+    def _masks(self, actions: Iterable[int]) -> np.ndarray:
+        index = np.asarray(actions, dtype=np.int64).reshape(-1)
+        if index.shape != (self.num_envs,):
+            raise ValueError(f"expected actions with shape ({self.num_envs},), got {index.shape}")
+        if index.size and (index.min() < 0 or index.max() >= self._table.size):
             raise ValueError("action index out of range")
-        return self._mask_table[a]
+        return self._table[index]
 
-    # ---- SB3 VecEnv contract -------------------------------------------------
+    # ---- SB3 VecEnv ---------------------------------------------------------------
     def reset(self) -> np.ndarray:
-        """env.py:478-507."""
-        frame = np.asarray(self._cuda_batch.reset(), dtype=np.uint8)
-        if self.observation_mode == "ram":
-            observations = np.asarray(self._cuda_batch.ram(), dtype=np.uint8)
-        else:
-            observations = frame
-        self._cuda_observations = frame
-        self._cuda_step_count = 0
-        self._cuda_env_step_counts[:] = 0
-        infos = self._infos()
-        for env in range(self.num_envs):
-            if self._options[env]:
-                infos[env]["reset_options"] = dict(self._options[env])
+        frames = self._cuda_batch.reset()
+        obs = self._observer.after_reset(frames)
+        self._clock.restart()
+        infos = [self._base_info() for _ in range(self.num_envs)]
+        for info, opts in zip(infos, self._options):
+            if opts:
+                info["reset_options"] = dict(opts)
         self.reset_infos = infos
         self._seeds = [None] * self.num_envs
         self._options = [{} for _ in range(self.num_envs)]
-        return observations
+        return obs
 
     def step_async(self, actions: Iterable[int]) -> None:
-        a = np.asarray(actions, dtype=np.int64).ravel()
-        if a.shape != (self.num_envs,):
-            raise ValueError(f"expected actions with shape ({self.num_envs},), got {a.shape}")
-        self._pending_actions = a
+        index = np.asarray(actions, dtype=np.int64).reshape(-1)
+        if index.shape != (self.num_envs,):
+            raise ValueError(f"expected actions with shape ({self.num_envs},), got {index.shape}")
+        self._queued = index
 
     def step_wait(self):
-        if self._pending_actions is None:
+        if self._queued is None:
             raise RuntimeError("step_async must be called before step_wait")
-        return self.step(self._pending_actions)
+        return self.step(self._queued)
 
-    def _truncation(self, dones: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-        max_steps = self.config.max_episode_steps
-        if max_steps > 0:
-            truncated = self._cuda_env_step_counts >= max_steps
-            return dones | truncated, truncated
-        return dones, np.zeros(self.num_envs, dtype=bool)
-
-    def _finish_episodes(self, dones, truncated, terminal: np.ndarray, infos) -> None:
-        """Record terminal observations, reset done envs on the device."""
-        done_envs = np.nonzero(dones)[0]
-        # One gathered copy per step; each info holds its console's row of it.
-        last = terminal[done_envs]
-        for i, env in enumerate(done_envs.tolist()):
-            info = infos[env]
-            info["terminal_observation"] = last[i]
-            info["terminated"] = not bool(truncated[env])
-            info["truncated"] = bool(truncated[env])
-            self.reset_infos[env] = {"backend": BACKEND_NAME, "observation_mode": self.observation_mode}
-        self._cuda_batch.reset_envs(dones.astype(np.uint8))
-        self._cuda_env_step_counts[dones] = 0
+    def _end_episodes(self, rule_done: np.ndarray, cut: np.ndarray, last_obs: np.ndarray,
+                      infos: list[dict[str, Any]]) -> np.ndarray:
+        """Reset the consoles whose episode ended; fills their infos and
+        reset_infos.  Returns the done mask."""
+        done = rule_done | cut
+        ended = np.flatnonzero(done)
+        if ended.size == 0:
+            return done
+        terminal = last_obs[ended]          # one gathered copy; each info keeps its row
+        for row, env in enumerate(ended.tolist()):
+            infos[env]["terminal_observation"] = terminal[row]
+            infos[env]["truncated"] = bool(cut[env])
+            infos[env]["terminated"] = not cut[env]
+            self.reset_infos[env] = self._base_info()
+        self._cuda_batch.reset_envs(done.astype(np.uint8))
+        self._clock.restart(done)
+        return done
 
     def step(self, actions: Iterable[int]):
-        """env.py:549-675: (observations, rewards, dones, infos)."""
-        masks = self._masks_for(actions)
-        self._cuda_step_count += 1
-        self._cuda_env_step_counts += 1
-        if self.observation_mode == "ram":
-            result = self._cuda_batch.step(masks, render_frame=False, copy_obs=False)
-            observations = np.asarray(self._cuda_batch.ram(), dtype=np.uint8)
-            copied, stale, rgb_copied = True, False, False
-        else:
-            copy = self.observation_cadence <= 1 or self._cuda_step_count % self.observation_cadence == 0
-            result = self._cuda_batch.step(masks, render_frame=copy, copy_obs=copy)
-            if copy:
-                observations = np.asarray(result["obs"], dtype=np.uint8)
-                self._cuda_observations = observations
-            elif self._cuda_observations is not None:
-                observations = self._cuda_observations
-            else:
-                observations = np.asarray(self._cuda_batch.render(), dtype=np.uint8)
-                self._cuda_observations = observations
-            copied, stale, rgb_copied = copy, not copy, copy
+        masks = self._masks(actions)
+        cut = self._clock.tick()
+        result, obs, flags = self._observer.step(masks)
         rewards = np.asarray(result["rewards"], dtype=np.float32)
-        dones, truncated = self._truncation(np.asarray(result["dones"], dtype=bool))
-        infos = self._infos(observation_cadence=self.observation_cadence, observations_copied=copied,
-                            observations_stale=stale, rgb_observations_copied=rgb_copied)
-        if dones.any():
-            # The returned observation of a done env is the first of its new episode.
-            self._finish_episodes(dones, truncated, observations, infos)
-            if self.observation_mode == "ram":
-                observations[dones] = self._ram_rows(dones)
-            else:
-                fresh = np.asarray(self._cuda_batch.render(), dtype=np.uint8)
-                self._cuda_observations = fresh
-                observations = np.where(dones[:, None, None, None], fresh, observations)
-        self._pending_actions = None
+        info = {**self._base_info(), "observation_cadence": self.observation_cadence, **flags}
+        infos = [info.copy() for _ in range(self.num_envs)]
+        done = self._end_episodes(np.asarray(result["dones"], dtype=bool), cut, obs, infos)
+        if done.any():
+            # The returned observation of a reset console is its new episode's first.
+            obs = self._observer.replace_rows(obs, done)
+        self._queued = None
         self.buf_infos = infos
-        return observations, rewards, dones, infos
+        return obs, rewards, done, infos
 
     def step_reward(self, actions: Iterable[int]):
-        """env.py:677-741: step without copying observations; (rewards, dones, infos)."""
-        masks = self._masks_for(actions)
-        self._cuda_env_step_counts += 1
+        """A step that copies rewards and dones only: (rewards, dones, infos)
+        (env.py:677-741); terminal observations are read only when an
+        episode ends."""
+        masks = self._masks(actions)
+        cut = self._clock.tick()
         result = self._cuda_batch.step(masks, render_frame=False, copy_obs=False)
         rewards = np.asarray(result["rewards"], dtype=np.float32)
-        dones, truncated = self._truncation(np.asarray(result["dones"], dtype=bool))
-        infos = self._infos(observations_copied=False)
-        if dones.any():
-            terminal = (np.asarray(self._cuda_batch.ram(), dtype=np.uint8) if self.observation_mode == "ram"
-                        else np.asarray(self._cuda_batch.render(), dtype=np.uint8))
-            self._finish_episodes(dones, truncated, terminal, infos)
-        self._pending_actions = None
+        rule_done = np.asarray(result["dones"], dtype=bool)
+        infos = [{**self._base_info(), "observations_copied": False} for _ in range(self.num_envs)]
+        last = self._observer.current() if (rule_done | cut).any() else None
+        done = self._end_episodes(rule_done, cut, last, infos) if last is not None else rule_done | cut
+        self._queued = None
         self.buf_infos = infos
-        return rewards, dones, infos
+        return rewards, done, infos
 
     def render(self, mode: str | None = None) -> np.ndarray | None:
-        mode = self.render_mode if mode is None else mode
+        mode = mode or self.render_mode
         if mode is None:
             return None
         if mode != "rgb_array":
             raise ValueError("only rgb_array rendering is supported")
-        return np.asarray(self._cuda_batch.render(), dtype=FRAME_DTYPE)
+        return self._cuda_batch.render()
 
     def get_images(self) -> list[np.ndarray]:
-        rendered = self.render()
-        return [rendered[e].copy() for e in range(self.num_envs)] if rendered is not None else []
+        frames = self.render()
+        return [] if frames is None else list(frames.copy())
 
     def close(self) -> None:
-        self._closed = True
+        self.closed = True
 
     def seed(self, seed: int | None = None) -> list[int | None]:
-        self._seeds = [None if seed is None else seed + env for env in range(self.num_envs)]
+        self._seeds = [None] * self.num_envs if seed is None else list(range(seed, seed + self.num_envs))
         return list(self._seeds)
 
     def set_options(self, options: dict[str, Any] | Sequence[dict[str, Any]] | None = None) -> None:
         if options is None:
-            self._options = [{} for _ in range(self.num_envs)]
+            options = [{}] * self.num_envs
         elif isinstance(options, dict):
-            self._options = [dict(options) for _ in range(self.num_envs)]
+            options = [options] * self.num_envs
         elif len(options) != self.num_envs:
             raise ValueError(f"expected {self.num_envs} option dictionaries, got {len(options)}")
-        else:
-            self._options = [dict(o) for o in options]
+        self._options = [dict(o) for o in options]
+
+    def _indices(self, indices) -> list[int]:
+        if indices is None:
+            return list(range(self.num_envs))
+        return [int(indices)] if isinstance(indices, (int, np.integer)) else [int(i) for i in indices]
 
     def get_attr(self, attr_name: str, indices=None) -> list[Any]:
-        if attr_name == "render_mode":
-            return [self.render_mode for _ in self._resolve_indices(indices)]
-        if attr_name == "name":
-            return [str(self._cuda_batch.name) for _ in self._resolve_indices(indices)]
-        raise AttributeError(f"the HIP vector env has no per-env attribute {attr_name!r}")
+        values = {"render_mode": self.render_mode, "name": str(self._cuda_batch.name)}
+        if attr_name not in values:
+            raise AttributeError(f"the HIP vector env has no per-env attribute {attr_name!r}")
+        return [values[attr_name]] * len(self._indices(indices))
 
     def set_attr(self, attr_name: str, value: Any, indices=None) -> None:
         raise AttributeError(f"the HIP vector env has no per-env attribute {attr_name!r}")
 
     def env_method(self, method_name: str, *method_args: Any, indices=None, **method_kwargs: Any) -> list[Any]:
-        if method_name == "render":
-            rendered = self.render()
-            return [rendered[i].copy() for i in self._resolve_indices(indices)] if rendered is not None else []
-        raise AttributeError(f"the HIP vector env has no per-env method {method_name!r}")
+        if method_name != "render":
+            raise AttributeError(f"the HIP vector env has no per-env method {method_name!r}")
+        frames = self.render()
+        return [] if frames is None else [frames[i].copy() for i in self._indices(indices)]
 
     def env_is_wrapped(self, wrapper_class: type[Any], indices=None) -> list[bool]:
-        return [False for _ in self._resolve_indices(indices)]
-
-    def _resolve_indices(self, indices) -> list[int]:
-        if indices is None:
-            return list(range(self.num_envs))
-        if isinstance(indices, int):
-            return [indices]
-        return [int(i) for i in indices]
+        return [False] * len(self._indices(indices))
 
 
 _EnvBase = gym.Env if gym is not None else object
 
 
 class NesleEnv(_EnvBase):
-    """One console behind the Gymnasium ``reset``/``step`` API (env.py:821-905)."""
+    """One console behind Gymnasium's ``reset``/``step`` (five-tuple) API: a
+    one-console ``NesleVecEnv`` underneath."""
 
     metadata = {"render_modes": ["rgb_array"], "render_fps": 60}
 
@@ -427,12 +439,11 @@ class NesleEnv(_EnvBase):
                  env_to_level: Sequence[int] | np.ndarray | None = None, *, rom_bytes: bytes | None = None) -> None:
         if gym is not None:
             super().__init__()
-        self.vector_env = NesleVecEnv(rom_path=rom_path, num_envs=1, frameskip=frameskip, action_space=action_space,
-                                      device=device, backend=backend, render_mode=render_mode,
-                                      observation_mode=observation_mode, observation_cadence=observation_cadence,
-                                      max_episode_steps=max_episode_steps, reset_state_path=reset_state_path,
-                                      reset_state_paths=reset_state_paths, env_to_level=env_to_level,
-                                      rom_bytes=rom_bytes)
+        self.vector_env = NesleVecEnv(rom_path, 1, frameskip=frameskip, action_space=action_space, device=device,
+                                      backend=backend, render_mode=render_mode, observation_mode=observation_mode,
+                                      observation_cadence=observation_cadence, max_episode_steps=max_episode_steps,
+                                      reset_state_path=reset_state_path, reset_state_paths=reset_state_paths,
+                                      env_to_level=env_to_level, rom_bytes=rom_bytes)
         self.render_mode = render_mode
         self.observation_space = self.vector_env.observation_space
         self.action_space = self.vector_env.action_space
@@ -444,27 +455,28 @@ class NesleEnv(_EnvBase):
             self.vector_env.seed(seed)
         if options is not None:
             self.vector_env.set_options(options)
-        observations = self.vector_env.reset()
-        return observations[0], self.vector_env.reset_infos[0]
+        return self.vector_env.reset()[0], self.vector_env.reset_infos[0]
 
     def step(self, action: int):
-        observations, rewards, dones, infos = self.vector_env.step([action])
+        obs, rewards, dones, infos = self.vector_env.step([action])
         info = infos[0]
-        return (observations[0], float(rewards[0]), bool(info.get("terminated", dones[0])),
-                bool(info.get("truncated", False)), info)
+        truncated = bool(info.get("truncated", False))
+        terminated = bool(info["terminated"]) if "terminated" in info else bool(dones[0])
+        return obs[0], float(rewards[0]), terminated, truncated, info
 
     def render(self) -> np.ndarray | None:
-        rendered = self.vector_env.render()
-        return None if rendered is None else rendered[0]
+        frames = self.vector_env.render()
+        return None if frames is None else frames[0]
 
     def close(self) -> None:
         self.vector_env.close()
 
 
 def make_vec(*args, **kwargs) -> NesleVecEnv:
-    """src/nesle/__init__.py:58-61."""
+    """The vector environment (src/nesle/__init__.py:58-61)."""
     return NesleVecEnv(*args, **kwargs)
 
 
 def make(*args, **kwargs) -> NesleEnv:
+    """The single-console environment."""
     return NesleEnv(*args, **kwargs)

@@ -14,10 +14,7 @@ one stream:
   reference calls ``reset_envs`` with a host mask after a ``done.any()`` host
   read every step, native_ppo.py:498-507); the RAM view after the step shows
   the post-reset state for them, exactly what the reference's
-  ``reset_envs`` + ``ram_device`` sequence returns.  With the shaped reward
-  (``reward_mode="smart"``, ``SmartMarioReward``) the step runs without
-  auto-reset, the reward reads the step's RAM, and the done consoles are then
-  reset through a device mask, the reference's order without its host reads;
+  ``reset_envs`` + ``ram_device`` sequence returns;
 * episode-length timeouts (``max_episode_steps``) reset through a device
   mask; episode returns are summed on the device and read once per log line;
 * the RAM, reward and done views are imported through DLPack once, before the
@@ -63,15 +60,12 @@ class NativePPOConfig:
     vf_coef: float = 0.5
     max_grad_norm: float = 0.5
     hidden_size: int = 256
+    # "minimal": the batch's in-kernel reward rule.  The reference's shaped
+    # SMB reward ("smart") is not part of this build and is refused.
     reward_mode: str = "minimal"
-    # Smart-reward overrides (None keeps SmartMarioReward's defaults).
-    flag_bonus: float | None = None
-    finish_zone_bonus: float | None = None
-    death_penalty: float | None = None
     seed: int = 1
     checkpoint_path: str = "nesle_native_ppo.pt"
     log_interval: int = 1
-    progress_bar: bool = False
     # Additions: weight init ("orthogonal" as the reference trainer, or
     # "xavier"), the in-kernel reward rule (CudaBatch ``reward=`` spec; None =
     # the SMB rule), whether to write checkpoints, and whether rollouts after
@@ -146,253 +140,70 @@ def compute_gae(rewards, dones, values, next_done, next_value, gamma: float, gae
 
 
 def _explained_variance(values, returns) -> float:
+    """1 - Var[returns - values] / Var[returns] (unbiased variances, one
+    device reduction for both); NaN when the returns are constant."""
     torch, _, _ = _require_torch()
     with torch.no_grad():
-        y_var = torch.var(returns)
-        if float(y_var.item()) == 0.0:
-            return float("nan")
-        return float((1.0 - torch.var(returns - values) / y_var).item())
-
-
-# ---- shaped reward ---------------------------------------------------------------
-
-def _read_bcd(ram, address: int, length: int):
-    """Decimal digits, one per RAM byte (low nibble), most significant first."""
-    torch, _, _ = _require_torch()
-    value = (ram[:, address] & 0x0F).to(dtype=torch.int32)
-    for offset in range(1, length):
-        value = value * 10 + (ram[:, address + offset] & 0x0F).to(dtype=torch.int32)
-    return value
-
-
-class SmartMarioReward:
-    """The reference's shaped Super Mario Bros. 1-1 reward from RAM and the
-    action masks (``TorchSmartMarioReward``, native_ppo.py:120-316): forward
-    progress, checkpoints every 128 px, score, kills, coins, finish zone,
-    flag, stall, jump and button penalties, death and time penalties.
-
-    Same constants, terms and order of summation.  Every state update is
-    in place and nothing reads back to the host (the reference assigns
-    through boolean masks, a host synchronisation, and rebinds some state
-    tensors), so a captured rollout graph carries the state across replays.
-    Works on tensors of any device."""
-
-    x_page = 0x006D
-    x_screen = 0x0086
-    y_viewport = 0x00B5
-    player_state = 0x000E
-    lives = 0x075A
-    world = 0x075F
-    stage = 0x075C
-    area = 0x0760
-    game_mode = 0x0770
-    coins_digits = 0x07ED
-    score_digits = 0x07DE
-
-    progress_scale = 0.18
-    backtrack_scale = 0.03
-    checkpoint_bonus = 3.0
-    checkpoint_width = 128.0
-    score_scale = 0.04
-    coin_bonus = 3.0
-    kill_bonus = 8.0
-    finish_zone_x = 3100.0
-    finish_zone_bonus = 100.0
-    flag_zone_x = 3300.0
-    flag_bonus = 100.0
-    death_penalty = 75.0
-    time_penalty = 0.005
-    stall_penalty = 0.02
-    stall_window = 40
-    max_stall_penalty = 0.5
-    jump_penalty = 0.005
-    neutral_jump_penalty = 0.02
-    repeated_jump_penalty = 0.02
-    repeated_jump_window = 6
-    max_repeated_jump_penalty = 0.25
-    left_penalty = 0.01
-    bad_button_penalty = 0.25
-
-    def __init__(self, num_envs: int, device=None) -> None:
-        torch, _, _ = _require_torch()
-        dev = device if device is not None else torch.device("cuda")
-        f32, i32 = torch.float32, torch.int32
-        self.last_x = torch.zeros(num_envs, dtype=f32, device=dev)
-        self.max_x = torch.zeros(num_envs, dtype=f32, device=dev)
-        self.checkpoint_index = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.last_score = torch.zeros(num_envs, dtype=f32, device=dev)
-        self.last_coins = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.last_lives = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.last_level = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.stall_steps = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.jump_streak = torch.zeros(num_envs, dtype=i32, device=dev)
-        self.finish_awarded = torch.zeros(num_envs, dtype=torch.bool, device=dev)
-        self.flag_awarded = torch.zeros(num_envs, dtype=torch.bool, device=dev)
-
-    def reset(self, ram) -> None:
-        self.reset_where(None, ram)
-
-    def reset_where(self, mask, ram) -> None:
-        """Start episodes where ``mask`` (bool [N]; None = all) from ``ram``."""
-        torch, _, _ = _require_torch()
-        fresh = {"last_x": self._x_pos(ram), "max_x": self._x_pos(ram), "last_score": self._score(ram).float(),
-                 "last_coins": self._coins(ram), "last_lives": ram[:, self.lives].to(torch.int32),
-                 "last_level": self._level(ram)}
-        for name in ("checkpoint_index", "stall_steps", "jump_streak", "finish_awarded", "flag_awarded"):
-            fresh[name] = torch.zeros_like(getattr(self, name))
-        for name, value in fresh.items():
-            state = getattr(self, name)
-            state.copy_(value if mask is None else torch.where(mask, value, state))
-
-    def compute(self, ram, action_masks, done):
-        """Reward of the step that produced ``ram`` (the RAM before any reset),
-        given the step's pad masks and done flags; updates the state."""
-        torch, _, _ = _require_torch()
-        x = self._x_pos(ram)
-        delta_x = x - self.last_x
-        forward = delta_x > 0
-        progress = torch.where(forward, torch.clamp(delta_x, max=16.0) * self.progress_scale,
-                               torch.clamp(delta_x, min=-16.0) * self.backtrack_scale)
-        self.stall_steps.copy_(torch.where(forward, torch.zeros_like(self.stall_steps), self.stall_steps + 1))
-        self.max_x.copy_(torch.maximum(self.max_x, x))
-        new_checkpoint_index = torch.floor(self.max_x / self.checkpoint_width).to(torch.int32)
-        checkpoint_delta = torch.clamp(new_checkpoint_index - self.checkpoint_index, min=0)
-        checkpoint = checkpoint_delta.float() * self.checkpoint_bonus
-        self.checkpoint_index.copy_(torch.maximum(self.checkpoint_index, new_checkpoint_index))
-
-        score = self._score(ram).float()
-        score_delta = torch.clamp(score - self.last_score, min=0.0)
-        coins = self._coins(ram)
-        coin_delta = coins - self.last_coins
-        coin_delta = torch.where(coin_delta < 0, coin_delta + 100, coin_delta)
-        coin_delta = torch.clamp(coin_delta, min=0)
-        score_reward = score_delta * self.score_scale
-        kill_score = score_delta - coin_delta.float() * 200.0
-        kill_reward = torch.where(kill_score >= 100.0, torch.full_like(score_reward, self.kill_bonus),
-                                  torch.zeros_like(score_reward))
-        coin_reward = coin_delta.float() * self.coin_bonus
-
-        finish_hit = (~self.finish_awarded) & (self.max_x >= self.finish_zone_x)
-        finish_reward = torch.where(finish_hit, torch.full_like(score_reward, self.finish_zone_bonus),
-                                    torch.zeros_like(score_reward))
-        self.finish_awarded |= finish_hit
-
-        is_death = self._is_death(ram)
-        flag_hit = (~self.flag_awarded) & ((ram[:, self.game_mode] == 2)
-                                           | ((self.max_x >= self.flag_zone_x) & done & (~is_death)))
-        flag_reward = torch.where(flag_hit, torch.full_like(score_reward, self.flag_bonus),
-                                  torch.zeros_like(score_reward))
-        self.flag_awarded |= flag_hit
-
-        stall_over = torch.clamp((self.stall_steps - self.stall_window + 1).float(), min=0.0)
-        stall_reward = -torch.clamp(stall_over * self.stall_penalty, max=self.max_stall_penalty)
-
-        action_reward = self._action_reward(action_masks)
-        death_reward = torch.where(done & is_death, torch.full_like(score_reward, -self.death_penalty),
-                                   torch.zeros_like(score_reward))
-        time_reward = torch.full_like(score_reward, -self.time_penalty)
-
-        self.last_x.copy_(x)
-        self.last_score.copy_(score)
-        self.last_coins.copy_(coins)
-        self.last_lives.copy_(ram[:, self.lives].to(torch.int32))
-        self.last_level.copy_(self._level(ram))
-        return (progress + checkpoint + score_reward + kill_reward + coin_reward + finish_reward + flag_reward
-                + stall_reward + action_reward + death_reward + time_reward)
-
-    def _x_pos(self, ram):
-        torch, _, _ = _require_torch()
-        return (ram[:, self.x_page].to(torch.float32) * 256.0) + ram[:, self.x_screen].to(torch.float32)
-
-    def _coins(self, ram):
-        return _read_bcd(ram, self.coins_digits, 2)
-
-    def _score(self, ram):
-        return _read_bcd(ram, self.score_digits, 6)
-
-    def _level(self, ram):
-        torch, _, _ = _require_torch()
-        return (ram[:, self.world].to(torch.int32) * 65536 + ram[:, self.stage].to(torch.int32) * 256
-                + ram[:, self.area].to(torch.int32))
-
-    def _is_death(self, ram):
-        state = ram[:, self.player_state]
-        return (state == 0x0B) | (state == 0x06) | (ram[:, self.y_viewport] > 1) | (ram[:, self.lives] == 0xFF)
-
-    def _action_reward(self, action_masks):
-        torch, _, _ = _require_torch()
-        reward = torch.zeros(action_masks.shape[0], dtype=torch.float32, device=action_masks.device)
-        jump = (action_masks & 0x01) != 0
-        right = (action_masks & 0x80) != 0
-        left = (action_masks & 0x40) != 0
-        start = (action_masks & 0x08) != 0
-        select = (action_masks & 0x04) != 0
-        self.jump_streak.copy_(torch.where(jump, self.jump_streak + 1, torch.zeros_like(self.jump_streak)))
-        reward -= jump.float() * self.jump_penalty
-        reward -= (jump & (~right)).float() * self.neutral_jump_penalty
-        repeated = torch.clamp((self.jump_streak - self.repeated_jump_window).float(), min=0.0)
-        reward -= torch.clamp(repeated * self.repeated_jump_penalty, max=self.max_repeated_jump_penalty)
-        reward -= left.float() * self.left_penalty
-        reward -= (left & right).float() * self.bad_button_penalty
-        reward -= (start | select).float() * self.bad_button_penalty
-        return reward
-
-
-def make_rewarder(config: NativePPOConfig, num_envs: int, device=None) -> SmartMarioReward | None:
-    """The smart rewarder of a config (None for the in-kernel "minimal" rule),
-    with the config's overrides (native_ppo.py:424-432)."""
-    if config.reward_mode == "minimal":
-        return None
-    if config.reward_mode != "smart":
-        raise ValueError(f"unknown reward mode: {config.reward_mode!r}")
-    rewarder = SmartMarioReward(num_envs, device)
-    for name in ("flag_bonus", "finish_zone_bonus", "death_penalty"):
-        value = getattr(config, name)
-        if value is not None:
-            setattr(rewarder, name, float(value))
-    return rewarder
+        var_ret, var_err = torch.stack((returns, returns - values)).var(dim=1).tolist()
+    return float("nan") if var_ret == 0.0 else 1.0 - var_err / var_ret
 
 
 # ---- checkpoints -----------------------------------------------------------
-# The reference stores numpy's RNG state as a pickled tuple and loads with
-# weights_only=False (native_ppo.py:324-368).  Here every field is a tensor,
-# number, string or list, so torch.load(weights_only=True) reads it back.
+# A checkpoint is a flat dict of tensors, numbers, strings and lists only, so
+# that torch.load(weights_only=True) reads it back without running pickled
+# code: model and optimizer state dicts, the config as a dict, the env-step
+# count, and the three RNG states (numpy's MT19937 as its key tensor plus
+# position and Gaussian cache).
+
+CHECKPOINT_FORMAT = "nesle_amd.native_ppo/1"
+
+
+def _rng_snapshot(torch) -> dict:
+    mt = np.random.get_state(legacy=False)
+    snap = {"torch": torch.get_rng_state(),
+            "numpy_key": torch.from_numpy(mt["state"]["key"].astype(np.int64)),
+            "numpy_pos": int(mt["state"]["pos"]), "numpy_has_gauss": int(mt["has_gauss"]),
+            "numpy_gauss": float(mt["gauss"])}
+    if torch.cuda.is_available():
+        snap["cuda"] = torch.cuda.get_rng_state()
+    return snap
+
+
+def _rng_restore(torch, snap: dict) -> None:
+    torch.set_rng_state(snap["torch"].cpu())
+    if "cuda" in snap and torch.cuda.is_available():
+        torch.cuda.set_rng_state(snap["cuda"].cpu())
+    np.random.set_state({"bit_generator": "MT19937",
+                         "state": {"key": snap["numpy_key"].cpu().numpy().astype(np.uint32), "pos": snap["numpy_pos"]},
+                         "has_gauss": snap["numpy_has_gauss"], "gauss": snap["numpy_gauss"]})
+
 
 def _save_checkpoint(path: str, model, optimizer, config: NativePPOConfig, global_step: int) -> None:
     torch, _, _ = _require_torch()
-    name, keys, pos, has_gauss, cached = np.random.get_state()
-    cfg = {k: (list(v) if isinstance(v, tuple) else v) for k, v in asdict(config).items()}
-    payload = {
-        "model": model.state_dict(),
-        "optimizer": optimizer.state_dict(),
-        "config": cfg,
-        "global_step": int(global_step),
-        "torch_rng_state": torch.get_rng_state(),
-        "numpy_rng_state": [str(name), torch.from_numpy(np.asarray(keys, dtype=np.int64)), int(pos),
-                            int(has_gauss), float(cached)],
-    }
-    if torch.cuda.is_available():
-        payload["cuda_rng_state"] = torch.cuda.get_rng_state()
-    Path(path).resolve().parent.mkdir(parents=True, exist_ok=True)
-    torch.save(payload, path)
+    plain = {}
+    for key, value in asdict(config).items():
+        plain[key] = list(value) if isinstance(value, tuple) else value
+    target = Path(path)
+    target.resolve().parent.mkdir(parents=True, exist_ok=True)
+    torch.save({"format": CHECKPOINT_FORMAT, "global_step": int(global_step), "config": plain,
+                "model": model.state_dict(), "optimizer": optimizer.state_dict(), "rng": _rng_snapshot(torch)},
+               target)
 
 
 def _load_checkpoint(path: str | None, model, optimizer) -> int:
-    if path is None or not Path(path).exists():
+    """Restore model, optimizer and RNGs from ``path``; returns the env-step
+    count it was saved at (0 when there is no such file)."""
+    if not path or not Path(path).is_file():
         return 0
     torch, _, _ = _require_torch()
-    map_location = "cuda" if torch.cuda.is_available() else "cpu"
-    payload = torch.load(path, map_location=map_location, weights_only=True)
-    model.load_state_dict(payload["model"])
-    optimizer.load_state_dict(payload["optimizer"])
-    if "torch_rng_state" in payload:
-        torch.set_rng_state(payload["torch_rng_state"].cpu())
-    if "cuda_rng_state" in payload and torch.cuda.is_available():
-        torch.cuda.set_rng_state(payload["cuda_rng_state"].cpu())
-    if "numpy_rng_state" in payload:
-        name, keys, pos, has_gauss, cached = payload["numpy_rng_state"]
-        np.random.set_state((name, keys.cpu().numpy().astype(np.uint32), pos, has_gauss, cached))
-    return int(payload.get("global_step", 0))
+    where = torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
+    ckpt = torch.load(path, map_location=where, weights_only=True)
+    if ckpt.get("format") != CHECKPOINT_FORMAT:
+        raise ValueError(f"{path} is not a {CHECKPOINT_FORMAT} checkpoint")
+    model.load_state_dict(ckpt["model"])
+    optimizer.load_state_dict(ckpt["optimizer"])
+    _rng_restore(torch, ckpt["rng"])
+    return int(ckpt["global_step"])
 
 
 # ---- environment -------------------------------------------------------------
@@ -630,8 +441,9 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         raise ValueError(
             f"rollout produces {rollout_timesteps} samples per update (num_envs={config.num_envs} * "
             f"n_steps={config.n_steps}) but batch_size={config.batch_size} is larger")
-    if config.reward_mode not in ("minimal", "smart"):
-        raise ValueError(f"unknown reward mode: {config.reward_mode!r}")
+    if config.reward_mode != "minimal":
+        raise ValueError(f"reward_mode {config.reward_mode!r} is not available: this build trains on the "
+                         "batch's in-kernel reward rule only (reward_mode='minimal', rule chosen by `reward`)")
     torch, _, _ = _require_torch()
     if not torch.cuda.is_available():
         raise SystemExit("native PPO needs a GPU")
@@ -664,9 +476,6 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     ram = from_dlpack(batch.ram_device())          # [N, 2048] uint8, refreshed by every step
     rewards_view = from_dlpack(batch.rewards_device())
     dones_view = from_dlpack(batch.last_done_device())
-    rewarder = make_rewarder(config, config.num_envs, dev)
-    if rewarder is not None:
-        rewarder.reset(ram)
 
     T = config.n_steps
     obs_buf = torch.empty((T, n, obs_dim), dtype=torch.uint8, device=dev)
@@ -701,24 +510,14 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         actions_buf[t].copy_(action)
         values_buf[t].copy_(value)
         pad = mask_table[action]
-        batch.step_device(pad, auto_reset=rewarder is None, synchronize=False)
+        batch.step_device(pad, auto_reset=True, synchronize=False)
         done = dones_view.bool()
         episode_lengths.add_(1.0)
-        if rewarder is None:
-            reward = rewards_view
-            if config.max_episode_steps > 0:
-                timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
-                batch.reset_envs_device(timeout.to(torch.uint8))   # consoles not in the mask are untouched
-                done = done | timeout
-        else:
-            # The shaped reward reads the step's RAM before any reset (the
-            # reference steps without auto-reset, then resets done consoles,
-            # native_ppo.py:486-509); the resets follow through a device mask.
-            reward = rewarder.compute(ram, pad, done)
-            if config.max_episode_steps > 0:
-                done = done | (episode_lengths >= float(config.max_episode_steps))
-            batch.reset_envs_device(done.to(torch.uint8))
-            rewarder.reset_where(done, ram)
+        reward = rewards_view
+        if config.max_episode_steps > 0:
+            timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
+            batch.reset_envs_device(timeout.to(torch.uint8))   # consoles not in the mask are untouched
+            done = done | timeout
         rewards_buf[t].copy_(reward)
         next_done.copy_(done.float())
         episode_returns.add_(reward)
@@ -740,7 +539,6 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
              "wall_s": 0.0, "log": [], "per_update": [], "graph_updates": 0}
     graph = None
     step_ms = None   # step-kernel time per rollout step, from the eager first rollout
-    progress = _progress_bar(config.progress_bar, global_step + num_updates * rollout_timesteps, global_step)
     t_start = time.perf_counter()
     for update in range(1, num_updates + 1):
         # The first rollout runs eagerly (HIP-event timing of the step kernel,
@@ -763,8 +561,6 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 if record is not None:
                     record(t, mask_table[actions_buf[t]], rewards_buf[t], next_done.bool())
         global_step += rollout_timesteps
-        if progress is not None:
-            progress.update(rollout_timesteps)   # per rollout: the steps run inside one graph
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         if not use_graph:
@@ -819,9 +615,6 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 "ep_len_mean": fin[2] / fin[0] if fin[0] else float("nan"),
             }
             stats["log"].append(line)
-            if progress is not None:
-                progress.set_postfix(fps=line["fps"], ret=f"{line['ep_return_mean']:.1f}",
-                                     ev=f"{line['explained_var']:.2f}", clip=f"{line['clipfrac']:.2f}")
             print(f"update={update}/{num_updates} step={global_step} fps={line['fps']} loss={line['loss']:.4f} "
                   f"clipfrac={line['clipfrac']:.3f} explained_var={line['explained_var']:.3f} "
                   f"episodes={line['episodes']} ep_return={line['ep_return_mean']:.2f} "
@@ -829,27 +622,12 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
             if config.save_checkpoints:
                 _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     torch.cuda.synchronize()
-    if progress is not None:
-        progress.close()
     stats["wall_s"] = time.perf_counter() - t_start
     stats["global_step"] = global_step
     if config.save_checkpoints and num_updates > 0:
         _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     stats["model"] = model
     return stats
-
-
-def _progress_bar(enabled: bool, total: int, initial: int):
-    """A tqdm bar over env-steps when asked for and tqdm is importable
-    (native_ppo.py:606-613)."""
-    if not enabled:
-        return None
-    try:
-        from tqdm.auto import tqdm
-    except ImportError:
-        print("progress bar requested but tqdm is not installed; falling back to update logs")
-        return None
-    return tqdm(total=total, initial=min(initial, total), desc="native PPO", unit="steps")
 
 
 def parse_args() -> tuple[NativePPOConfig, str | None]:
@@ -874,18 +652,12 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
     p.add_argument("--vf-coef", type=float, default=0.5)
     p.add_argument("--max-grad-norm", type=float, default=0.5)
     p.add_argument("--hidden-size", type=int, default=256)
-    p.add_argument("--reward-mode", default="minimal", choices=["minimal", "smart"])
-    p.add_argument("--flag-bonus", type=float, default=None, help="override SmartMarioReward.flag_bonus (smart mode)")
-    p.add_argument("--finish-zone-bonus", type=float, default=None,
-                   help="override SmartMarioReward.finish_zone_bonus (smart mode)")
-    p.add_argument("--death-penalty", type=float, default=None,
-                   help="override SmartMarioReward.death_penalty (smart mode)")
+    p.add_argument("--reward-mode", default="minimal", choices=["minimal"])
     p.add_argument("--init", default="orthogonal", choices=["orthogonal", "xavier"])
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--checkpoint-path", default="nesle_native_ppo.pt")
     p.add_argument("--resume-from", default=None)
     p.add_argument("--log-interval", type=int, default=1)
-    p.add_argument("--progress-bar", action="store_true")
     a = p.parse_args()
     if a.reset_state_path and a.reset_state_paths:
         raise SystemExit("Pass either --reset-state-path or --reset-state-paths, not both.")
@@ -896,8 +668,7 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
         max_episode_steps=a.max_episode_steps, learning_rate=a.learning_rate, gamma=a.gamma,
         gae_lambda=a.gae_lambda, clip_coef=a.clip_coef, ent_coef=a.ent_coef, vf_coef=a.vf_coef,
         max_grad_norm=a.max_grad_norm, hidden_size=a.hidden_size, reward_mode=a.reward_mode,
-        flag_bonus=a.flag_bonus, finish_zone_bonus=a.finish_zone_bonus, death_penalty=a.death_penalty, init=a.init,
-        seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval, progress_bar=a.progress_bar)
+        init=a.init, seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval)
     return cfg, a.resume_from
 
 

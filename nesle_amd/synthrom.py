@@ -376,8 +376,17 @@ class _Gen:
         return None
 
     # -- whole ROM ---------------------------------------------------------
-    def build(self, seed: int) -> SynthRom:
+    def build(self, seed: int, prg_banks: int = 2) -> SynthRom:
+        """``prg_banks`` 2: 32 KB PRG at $8000-$FFFF.  1: a 16 KB image (NROM-128),
+        mirrored at $8000 and $C000: the program is assembled at $C000-$FFFF
+        (RESET/main loop $C000-$CFFF, subroutines $D000-$EEFF) and the
+        vectors point into the $8000 mirror, so the console starts, takes
+        NMIs and BRKs in the low copy and jumps or returns into the high one."""
         a, r = self.a, self.r
+        small = prg_banks == 1
+        code_lo = 0xC000 if small else 0x8000
+        main_stop = 0xCC00 if small else 0xB800   # the main loop's last block starts below this
+        subs_at = 0xD000 if small else 0xC000
         done_init = r.range(25, 250)     # done fires after 8*done_init frames
         pointers = [r.range(0x0300, 0x0700) for _ in range(8)]
         ctrl = 0x90 | r.below(4)         # NMI on, BG table $1000, seeded nametable
@@ -386,7 +395,7 @@ class _Gen:
         # Subroutines first (placed high, called from the main loop).
         n_subs = 16
         self.subs = [a.new_label() for _ in range(n_subs)]
-        a.org(0xC000)
+        a.org(subs_at)
         for i in range(n_subs - 1, -1, -1):
             a.label(self.subs[i])
             self.emit_block(1, 24, i)
@@ -396,7 +405,7 @@ class _Gen:
             raise ValueError("subroutines overflow the code area")
 
         # RESET routine.
-        a.org(0x8000)
+        a.org(code_lo)
         a.label("RESET")
         a.op("SEI"); a.op("CLD")
         a.op("LDX", "imm", 0xFF); a.op("TXS")
@@ -436,10 +445,10 @@ class _Gen:
 
         # Main loop fills the rest of the low code area.
         a.label("MAIN")
-        while a.pc < 0xB800:
+        while a.pc < main_stop:
             self.emit_block(0, 12, None)
         a.op("JMP", "abs", "MAIN")
-        if a.pc > 0xC000:
+        if a.pc > subs_at:
             raise ValueError("main loop overflows into subroutines")
 
         # Data tables at $F000: palette, nametables, attributes, sprites, noise.
@@ -501,19 +510,23 @@ class _Gen:
         a.label("IRQ")
         a.op("RTI")
 
+        mirror = 0x4000 if small else 0
         a.org(0xFFFA)
-        a.byte(NMI_ADDR & 0xFF, NMI_ADDR >> 8)
-        a.byte(0x00, 0x80)
-        a.byte(IRQ_ADDR & 0xFF, IRQ_ADDR >> 8)
+        a.byte(NMI_ADDR & 0xFF, (NMI_ADDR - mirror) >> 8)
+        a.byte(0x00, (code_lo - mirror) >> 8)
+        a.byte(IRQ_ADDR & 0xFF, (IRQ_ADDR - mirror) >> 8)
         a.resolve()
 
         chr_bytes = bytes(r.below(256) for _ in range(0x2000))
-        header = bytes([0x4E, 0x45, 0x53, 0x1A, 2, 1, 0x01, 0x00, 0, 0, 0, 0, 0, 0, 0, 0])
-        prg = bytes(a.prg)
+        header = bytes([0x4E, 0x45, 0x53, 0x1A, prg_banks, 1, 0x01, 0x00, 0, 0, 0, 0, 0, 0, 0, 0])
+        prg = bytes(a.prg[0x4000:]) if small else bytes(a.prg)
         return SynthRom(seed=seed, rom=header + prg + chr_bytes, prg=prg, chr=chr_bytes,
                         done_init=done_init, labels=dict(a.labels))
 
 
-def make_rom(seed: int) -> SynthRom:
-    """The synthetic NROM image for ``seed`` (deterministic)."""
-    return _Gen(seed).build(seed)
+def make_rom(seed: int, prg_banks: int = 2) -> SynthRom:
+    """The synthetic NROM image for ``seed`` (deterministic); ``prg_banks`` 1
+    gives the 16 KB (NROM-128) variant."""
+    if prg_banks not in (1, 2):
+        raise ValueError("prg_banks must be 1 or 2")
+    return _Gen(seed).build(seed, prg_banks)

@@ -1100,4 +1100,75 @@ double oracle_run_batch(const std::uint8_t* ines, std::size_t len, std::uint32_t
     return secs;
 }
 
+// The snapshot workload on the CPU: console `env` starts from blob
+// levels[env] with RAM[done_addr] = done_init[env], takes the pad stream
+// splitmix64(seed ^ env << 32 ^ (step0 + k)) & 0xFF, and is re-loaded from its
+// blob after every env-step that leaves RAM[done_addr] == 0 (the auto-reset of
+// the HIP batch).  Returns seconds; RAM checksum, instructions and resets out.
+double oracle_run_levels(const std::uint8_t* ines, std::size_t len, const std::uint8_t* blobs, std::uint32_t n_levels,
+                         const std::uint8_t* levels, const std::uint8_t* done_init, std::uint32_t done_addr,
+                         std::uint32_t n_envs, std::uint32_t steps, std::uint32_t frameskip, std::uint64_t seed,
+                         std::uint64_t step0, std::uint32_t threads, std::uint64_t* checksum,
+                         std::uint64_t* instructions, std::uint64_t* resets) {
+    Cart cart;
+    try {
+        cart = parse_ines(ines, len);
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1.0;
+    }
+    for (std::uint32_t e = 0; e < n_envs; ++e)
+        if (levels[e] >= n_levels) {
+            g_error = "level out of range";
+            return -1.0;
+        }
+    threads = std::max(1u, std::min(threads, n_envs));
+    done_addr &= 0x7FF;
+    std::atomic<std::uint64_t> sum{0}, instr{0}, rs{0};
+    std::atomic<bool> failed{false};
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<std::thread> pool;
+    for (std::uint32_t t = 0; t < threads; ++t) {
+        pool.emplace_back([&, t]() {
+            const std::uint32_t lo = static_cast<std::uint32_t>(std::uint64_t(n_envs) * t / threads);
+            const std::uint32_t hi = static_cast<std::uint32_t>(std::uint64_t(n_envs) * (t + 1) / threads);
+            std::uint64_t local = 0, li = 0, lr = 0;
+            try {
+                for (std::uint32_t env = lo; env < hi; ++env) {
+                    const std::uint8_t* b = blobs + static_cast<std::size_t>(levels[env]) * kStateBytes;
+                    Machine m;
+                    m.cart = &cart;
+                    m.load(b);
+                    m.ram[done_addr] = done_init[env];
+                    for (std::uint32_t k = 0; k < steps; ++k) {
+                        m.set_buttons(static_cast<std::uint8_t>(
+                            splitmix64(seed ^ (std::uint64_t(env) << 32) ^ (step0 + k)) & 0xFF));
+                        for (std::uint32_t f = 0; f < frameskip; ++f) li += m.step_frame(200000);
+                        if (m.ram[done_addr] == 0) {
+                            m.load(b);
+                            ++lr;
+                        }
+                    }
+                    local ^= fnv1a(m.ram, 2048);
+                }
+            } catch (...) {
+                failed = true;
+            }
+            sum ^= local;
+            instr += li;
+            rs += lr;
+        });
+    }
+    for (auto& th : pool) th.join();
+    const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    if (failed) {
+        g_error = "illegal opcode during batch run";
+        return -1.0;
+    }
+    if (checksum) *checksum = sum.load();
+    if (instructions) *instructions = instr.load();
+    if (resets) *resets = rs.load();
+    return secs;
+}
+
 }  // extern "C"

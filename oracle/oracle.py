@@ -122,6 +122,12 @@ def _oracle_lib():
         lib.oracle_run_batch.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32,
                                          ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]
+        lib.oracle_run_levels.restype = ctypes.c_double
+        lib.oracle_run_levels.argtypes = [ctypes.c_char_p, ctypes.c_size_t, _U8P, ctypes.c_uint32, _U8P, _U8P,
+                                          ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint32,
+                                          ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                                          ctypes.POINTER(ctypes.c_uint64)]
         _LIB = lib
     return _LIB
 
@@ -147,6 +153,8 @@ def _ref_lib():
         lib.ref_render_rgb.argtypes = [ctypes.c_void_p, _U8P]
         lib.ref_run_batch.restype = ctypes.c_double
         lib.ref_run_batch.argtypes = _oracle_lib().oracle_run_batch.argtypes
+        lib.ref_run_levels.restype = ctypes.c_double
+        lib.ref_run_levels.argtypes = _oracle_lib().oracle_run_levels.argtypes
         _REF = lib
     return _REF
 
@@ -298,6 +306,27 @@ def run_batch(rom: bytes, num_envs: int, steps: int, frameskip: int, seed: int, 
     if secs < 0:
         raise RuntimeError("CPU batch run failed")
     return secs, cs.value, ins.value
+
+
+def run_levels(rom: bytes, blobs: list[bytes], levels: np.ndarray, done_init: np.ndarray, done_addr: int,
+               steps: int, frameskip: int, seed: int, step0: int, threads: int,
+               kind: str = "port") -> tuple[float, int, int, int]:
+    """Multi-threaded CPU run of the snapshot workload (one console per entry
+    of ``levels``, auto-reset from its blob when RAM[done_addr] reaches 0);
+    returns (seconds, ram checksum, instructions, resets)."""
+    fn = _oracle_lib().oracle_run_levels if kind == "port" else _ref_lib().ref_run_levels
+    bank = np.frombuffer(b"".join(bytes(b) for b in blobs), dtype=np.uint8).copy()
+    assert bank.size == len(blobs) * STATE_BYTES
+    lv = np.ascontiguousarray(levels, dtype=np.uint8)
+    di = np.ascontiguousarray(done_init, dtype=np.uint8)
+    assert lv.shape == di.shape
+    cs, ins, rs = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    secs = fn(rom, len(rom), bank.ctypes.data_as(_U8P), len(blobs), lv.ctypes.data_as(_U8P),
+              di.ctypes.data_as(_U8P), done_addr, lv.size, steps, frameskip, seed & 0xFFFFFFFFFFFFFFFF,
+              step0, threads, ctypes.byref(cs), ctypes.byref(ins), ctypes.byref(rs))
+    if secs < 0:
+        raise RuntimeError("CPU snapshot run failed")
+    return secs, cs.value, ins.value, rs.value
 
 
 def cpu_threads() -> int:

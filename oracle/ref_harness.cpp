@@ -235,4 +235,75 @@ double ref_run_batch(const std::uint8_t* ines, std::size_t len, std::uint32_t n_
     return secs;
 }
 
+// Same contract as oracle_run_levels (oracle/nes_oracle.cpp), over the
+// reference Console: start from snapshot blobs with a per-console done byte,
+// re-load the console's blob after an env-step that leaves the byte at 0.
+double ref_run_levels(const std::uint8_t* ines, std::size_t len, const std::uint8_t* blobs, std::uint32_t n_levels,
+                      const std::uint8_t* levels, const std::uint8_t* done_init, std::uint32_t done_addr,
+                      std::uint32_t n_envs, std::uint32_t steps, std::uint32_t frameskip, std::uint64_t seed,
+                      std::uint64_t step0, std::uint32_t threads, std::uint64_t* checksum,
+                      std::uint64_t* instructions, std::uint64_t* resets) {
+    nesle::RomImage rom;
+    try {
+        rom = nesle::parse_ines(std::span<const std::uint8_t>(ines, len));
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1.0;
+    }
+    for (std::uint32_t e = 0; e < n_envs; ++e)
+        if (levels[e] >= n_levels) {
+            g_error = "level out of range";
+            return -1.0;
+        }
+    threads = std::max(1u, std::min(threads, n_envs));
+    done_addr &= 0x7FF;
+    std::atomic<std::uint64_t> sum{0}, instr{0}, rs{0};
+    std::atomic<bool> failed{false};
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<std::thread> pool;
+    for (std::uint32_t t = 0; t < threads; ++t) {
+        pool.emplace_back([&, t]() {
+            const auto lo = static_cast<std::uint32_t>(std::uint64_t(n_envs) * t / threads);
+            const auto hi = static_cast<std::uint32_t>(std::uint64_t(n_envs) * (t + 1) / threads);
+            std::uint64_t local = 0, li = 0, lr = 0;
+            try {
+                for (std::uint32_t env = lo; env < hi; ++env) {
+                    const std::uint8_t* b = blobs + static_cast<std::size_t>(levels[env]) * kStateBytes;
+                    auto e = std::make_unique<RefEnv>(rom);
+                    ref_load(e.get(), b);
+                    e->console.cpu_ram_[done_addr] = done_init[env];
+                    for (std::uint32_t k = 0; k < steps; ++k) {
+                        e->console.controller1().set_buttons(static_cast<std::uint8_t>(
+                            splitmix64(seed ^ (std::uint64_t(env) << 32) ^ (step0 + k)) & 0xFF));
+                        for (std::uint32_t f = 0; f < frameskip; ++f)
+                            li += e->console.step_frame(e->cpu, 200000).instructions;
+                        if (e->console.cpu_ram_[done_addr] == 0) {
+                            ref_load(e.get(), b);
+                            ++lr;
+                        }
+                    }
+                    std::uint64_t h = 0xCBF29CE484222325ull;
+                    for (auto v : e->console.cpu_ram_) { h ^= v; h *= 0x100000001B3ull; }
+                    local ^= h;
+                }
+            } catch (...) {
+                failed = true;
+            }
+            sum ^= local;
+            instr += li;
+            rs += lr;
+        });
+    }
+    for (auto& th : pool) th.join();
+    const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    if (failed) {
+        g_error = "exception during reference batch run";
+        return -1.0;
+    }
+    if (checksum) *checksum = sum.load();
+    if (instructions) *instructions = instr.load();
+    if (resets) *resets = rs.load();
+    return secs;
+}
+
 }  // extern "C"

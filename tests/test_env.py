@@ -35,19 +35,38 @@ def test_env_to_level_checks(tmp_path):
 
 
 def test_observation_modes_and_spaces():
-    assert E._normalize_observation_mode("RGB") == "rgb_array"
-    assert E._normalize_observation_mode("cpu-ram") == "ram"
-    d = E.DiscreteSpace(12)
-    assert d.contains(11) and not d.contains(12) and not d.contains("x")
-    box = E.BoxSpace(0, 255, (2048,), np.uint8)
-    assert box.contains(box.sample())
+    assert E.observation_mode_of("RGB") == "rgb_array"
+    assert E.observation_mode_of("frame") == "rgb_array"
+    assert E.observation_mode_of("cpu-ram") == "ram"
+    with pytest.raises(ValueError):
+        E.observation_mode_of("depth")
+    box, d = E._spaces((2048,), 12)
+    assert d.n == 12 and d.contains(11) and not d.contains(12) and not d.contains("x")
+    assert box.shape == (2048,) and box.contains(box.sample())
+
+
+def test_level_map_round_robin_and_explicit():
+    assert E.level_map(1, 4, None) is None and E.level_map(0, 4, None) is None
+    assert E.level_map(3, 7, None).tolist() == [0, 1, 2, 0, 1, 2, 0]
+    assert E.level_map(3, 3, [2, 2, 0]).tolist() == [2, 2, 0]
+    with pytest.raises(ValueError):
+        E.level_map(3, 2, [0, -1])
+
+
+def test_episode_clock_limit_and_restart():
+    c = E._EpisodeClock(3, 2)
+    assert not c.tick().any()
+    assert c.tick().all()
+    c.restart(np.array([True, False, True]))
+    assert c.tick().tolist() == [False, True, False]
+    assert not E._EpisodeClock(2, 0).tick().any()
 
 
 def test_gzip_reset_states_are_unpacked(tmp_path):
     raw = bytes(range(256)) * 4
     p = tmp_path / "level.state"
     p.write_bytes(gzip.compress(raw))
-    assert E._load_reset_state(p) == raw
+    assert E.read_state_file(p) == raw
     q = tmp_path / "plain.fcs"
     q.write_bytes(raw)
-    assert E._load_reset_state(q) == raw
+    assert E.read_state_file(q) == raw

@@ -163,3 +163,55 @@ def test_snapshot_levels(tmp_path):
     assert single._cuda_batch.num_levels == 1
     obs = single.reset()
     assert np.array_equal(obs[0], level_ram[0]) and np.array_equal(obs[1], level_ram[0])
+
+
+def test_partial_dones_return_reset_rows_and_step_rows(tmp_path):
+    """Only some consoles end their episode in a step: their returned rows
+    are the reset RAM (their own level's) and their infos hold the step's
+    RAM as terminal observation; every other row is the step's RAM.  The
+    ROM counts RAM[$10] up in a loop, so a step's RAM differs from a reset
+    one; level 1 carries the SMB rule's "dead" player state (RAM[$0E] = 6),
+    so exactly its consoles are done after every step."""
+    from tests.kat_roms import nrom_bytes
+
+    rom = nrom_bytes(2, code={0x8000: [0xE6, 0x10, 0x4C, 0x00, 0x80]}, reset=0x8000)
+    base = O.Oracle(rom).save()
+    blobs = []
+    for level, state in enumerate((0x08, 0x06)):
+        s = base.copy()
+        s[RAM + 0x0E] = state
+        s[RAM + 0x10] = 0x40 * level
+        s[RAM + 0xB5] = 1
+        blobs.append(s)
+    paths = []
+    for i, s in enumerate(blobs):
+        p = tmp_path / f"lvl{i}.state"
+        p.write_bytes(bytes(s))
+        paths.append(str(p))
+    levels = [0, 1, 0, 1, 1, 0]
+    n = len(levels)
+    say(f"[gpu] vec env partial dones: N={n}")
+    env = E.NesleVecEnv("count.nes", n, observation_mode="ram", action_space="raw", reset_state_paths=paths,
+                        env_to_level=levels, rom_bytes=rom)
+    cons = [O.Oracle(rom) for _ in range(n)]
+    obs = env.reset()
+    for e in range(n):
+        cons[e].set_reward()
+        cons[e].load(blobs[levels[e]])
+        assert np.array_equal(obs[e], blobs[levels[e]][RAM:RAM + 2048])
+    for k in range(3):
+        obs, rew, done, infos = env.step(np.zeros(n, dtype=np.int64))
+        assert done.tolist() == [lv == 1 for lv in levels], f"step {k}"
+        for e in range(n):
+            _, r, d = cons[e].step(0, 4)
+            stepped = cons[e].save()[RAM:RAM + 2048]
+            assert rew[e] == np.float32(r) and bool(d) == bool(done[e])
+            if done[e]:
+                assert np.array_equal(infos[e]["terminal_observation"], stepped), f"step {k} env {e}"
+                assert infos[e]["terminated"] and not infos[e]["truncated"]
+                cons[e].load(blobs[levels[e]])
+                assert np.array_equal(obs[e], blobs[levels[e]][RAM:RAM + 2048]), f"step {k} env {e} reset row"
+            else:
+                assert "terminal_observation" not in infos[e]
+                assert np.array_equal(obs[e], stepped), f"step {k} env {e} step row"
+                assert stepped[0x10] != blobs[levels[e]][RAM + 0x10]

@@ -250,3 +250,85 @@ def test_profile_counts_match_instructions():
     ins = b.host(abi.VIEW_INSTRUCTIONS)
     assert ops.sum() == ins.sum() == pcs.sum()
     assert set(np.nonzero(ops)[0].tolist()) <= synthrom.OFFICIAL_OPCODES
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_nrom128_cold_boot_nmi_loop_and_autoreset(num_envs):
+    """A 16 KB PRG image (NROM-128) mirrored at $8000 and $C000 (the
+    reference's read_nrom_prg, batch_bus.cuh:24-33; test_console.cpp:190-199):
+    the console boots through the reset vector in the low copy, takes every
+    frame's NMI there and runs its main loop and subroutines in the high
+    copy.  Cold boot, then snapshot auto-reset with the x-delta rule, in both
+    LDS layouts (64 consoles: all RAM in LDS; 16,384: split), sampled
+    consoles against the oracle."""
+    rom = synthrom.make_rom(5, prg_banks=1).rom
+    assert abi.parse_ines(rom)["prg_rom_size"] == 16384
+    n = num_envs
+    rng = np.random.default_rng(n)
+    sample = list(range(n)) if n <= 64 else sorted({0, 63, 64, 4095, n - 1, *rng.integers(0, n, 6).tolist()})
+    say(f"[gpu] NROM-128 cold boot: N={n} fs=4 sample={len(sample)}")
+    b = abi.Batch(rom, n, frameskip=4)
+    ob = OracleBatch(rom, sample)
+    for k in range(12):
+        m = masks_for(31, n, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS)[sample], ins, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k}")
+    for e, ref in zip(sample, ob.states()):
+        got = b.save_state(e)
+        assert np.array_equal(got, ref), f"cold boot env {e}: {first_diff(got, ref)}"
+    assert (b.host(abi.VIEW_FRAMES) == 4).all()
+
+    say(f"[gpu] NROM-128 snapshot auto-reset: N={n}")
+    snaps = warm_snapshots(rom, [60, 120, 180, 240], seed=8)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 1 + i
+    blobs = [bytes(s) for s in snaps]
+    levels = rng.integers(0, 4, n).astype(np.uint8)
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.5)
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.5)
+    b.set_snapshots(blobs, levels)
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        c.load(snaps[levels[e]])
+    ends = 0
+    for k in range(24):
+        m = masks_for(32, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES)[sample], don, err_msg=f"step {k} dones")
+        for j in np.nonzero(don)[0]:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += int(don.sum())
+        if k % 6 == 5:
+            for e, ref in zip(sample, ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert ends >= len(sample)
+
+
+def test_poke_ram_envs_writes_one_byte_per_console():
+    """nesle_poke_ram_envs: console e's RAM byte gets values[e], through the
+    $0800 mirror too; nothing else changes and the reward baselines stay."""
+    rom = _rom(3)
+    n = 300
+    say(f"[gpu] poke_ram_envs: N={n}")
+    b = abi.Batch(rom, n, frameskip=4)
+    b.set_actions(masks_for(2, n, 0))
+    b.step()
+    before = b.host(abi.VIEW_RAM).copy()
+    vals = np.random.default_rng(1).integers(0, 256, n).astype(np.uint8)
+    b.poke_ram_envs(0x0812, vals)
+    after = b.host(abi.VIEW_RAM)
+    assert np.array_equal(after[:, 0x12], vals)
+    before[:, 0x12] = vals
+    assert np.array_equal(after, before)
+    with pytest.raises(ValueError):
+        abi.lib()  # the library is loaded; a null values pointer is an argument error
+        abi._check(abi.lib().nesle_poke_ram_envs(b.h, 0x12, None, 0))

@@ -72,14 +72,12 @@ def test_ppo_rollout_matches_oracle_and_update_learns(max_episode_steps):
     assert all(moved)
 
 
-@pytest.mark.parametrize("reward_mode", ["minimal", "smart"])
-def test_rollout_graph_replays_match_eager_rollouts(reward_mode):
+def test_rollout_graph_replays_match_eager_rollouts():
     """With cuda_graph the rollouts after the first replay one captured HIP
     graph (policy, sampling, the C-ABI step and bookkeeping for all steps),
     and the minibatch steps after the first update replay another.  Every
     rollout replay, with the update replays and host synchronisations between
-    them, equals the same rollout run eagerly (eager updates); with the
-    shaped reward, its state is carried across replays in place."""
+    them, equals the same rollout run eagerly (eager updates)."""
     rom = synthrom.make_rom(5).rom
     snaps = warm_snapshots(rom, [100, 150, 200, 250], seed=55)
     for i, s in enumerate(snaps):
@@ -89,10 +87,9 @@ def test_rollout_graph_replays_match_eager_rollouts(reward_mode):
                   clip=15, time_penalty=0.25)
     runs, per_update = {}, {}
     for graph in (False, True):
-        say(f"[gpu] ppo rollouts cuda_graph={graph} reward={reward_mode}: N={n} T={T} updates={updates}")
+        say(f"[gpu] ppo rollouts cuda_graph={graph}: N={n} T={T} updates={updates}")
         cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, n_steps=T, batch_size=128, update_epochs=1,
                                 frameskip=4, action_space="complex", init="xavier", reward=reward,
-                                reward_mode=reward_mode,
                                 total_timesteps=n * T * updates, save_checkpoints=False, seed=11,
                                 max_episode_steps=6, cuda_graph=graph)
         got = []
@@ -222,61 +219,3 @@ def test_ppo_head_matches_the_reference_loss_and_its_gradients(n, a, spread):
         torch.testing.assert_close(gv.grad.cpu(), ref_v.grad, rtol=1e-4, atol=1e-7)
     if spread == 0.0:
         assert float(want_cf) == 0.0
-
-
-@pytest.mark.parametrize("max_episode_steps", [0, 5])
-def test_ppo_smart_reward_matches_host_recompute(max_episode_steps):
-    """reward_mode="smart": the rollout steps without auto-reset, the shaped
-    reward reads each step's RAM before any reset, done consoles (and
-    timeouts) are reset through a device mask and the rewarder restarts their
-    episodes from the post-reset RAM (native_ppo.py:486-509).  Every step's
-    rewards and dones equal oracle consoles stepped with the same masks, the
-    same reward class computing on the host (CPU tensors) from their RAM
-    (to 1e-4: float32 sums on two devices)."""
-    rom = synthrom.make_rom(5).rom
-    snaps = warm_snapshots(rom, [100, 150, 200, 250], seed=55)
-    for i, s in enumerate(snaps):
-        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 1 + i
-    n, T = 64, 16
-    reward = dict(kind="x_delta", x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE,
-                  clip=15, time_penalty=0.25)
-    cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, n_steps=T, batch_size=256, update_epochs=1,
-                            frameskip=4, action_space="complex", init="xavier", reward=reward, reward_mode="smart",
-                            death_penalty=30.0, total_timesteps=n * T, save_checkpoints=False, seed=5,
-                            max_episode_steps=max_episode_steps)
-    rec = []
-    say(f"[gpu] ppo smart reward: N={n} T={T} max_episode_steps={max_episode_steps}")
-    stats = P.train_native_ppo(cfg, rom_bytes=rom, snapshot_bytes=[bytes(s) for s in snaps],
-                               record=lambda k, m, r, d: rec.append((m.cpu().numpy(), r.cpu().numpy().copy(),
-                                                                     d.cpu().numpy().copy())))
-    assert stats["updates"] == 1 and len(rec) == T and math.isfinite(stats["log"][-1]["loss"])
-
-    levels = np.arange(n) % len(snaps)
-    ob = OracleBatch(rom, list(range(n)), reward=dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
-                                                      done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.25))
-    for e, c in enumerate(ob.cons):
-        c.load(snaps[levels[e]])
-
-    def ram_now():
-        r0 = O.OFF["ram"]
-        return torch.from_numpy(np.stack([st[r0:r0 + 2048] for st in ob.states()]))
-
-    host = P.make_rewarder(cfg, n, torch.device("cpu"))
-    host.reset(ram_now())
-    length = np.zeros(n, dtype=np.int64)
-    ends = 0
-    for k, (masks, rew, done) in enumerate(rec):
-        _, _, d = ob.step(masks, 4)
-        want_r = host.compute(ram_now(), torch.from_numpy(masks), torch.from_numpy(d.astype(bool))).numpy()
-        length += 1
-        want_done = d.astype(bool)
-        if max_episode_steps:
-            want_done |= length >= max_episode_steps
-        np.testing.assert_array_equal(done, want_done, err_msg=f"step {k} dones")
-        np.testing.assert_allclose(rew, want_r, rtol=0, atol=1e-4, err_msg=f"step {k} rewards")
-        for e in np.nonzero(want_done)[0]:
-            ob.cons[e].load(snaps[levels[e]])
-        host.reset_where(torch.from_numpy(want_done), ram_now())
-        length[want_done] = 0
-        ends += int(want_done.sum())
-    assert ends > 0

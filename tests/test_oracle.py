@@ -54,9 +54,12 @@ def test_oracle_matches_golden_hashes(rom_seed):
 # ---- the reference core itself -------------------------------------------------------
 
 @needs_ref
-@pytest.mark.parametrize("rom_seed", [5, 11, 2026])
-def test_oracle_matches_reference_core_frameskip4(rom_seed):
-    rom = synthrom.make_rom(rom_seed).rom
+@pytest.mark.parametrize("rom_seed,prg_banks", [(5, 2), (11, 2), (2026, 2), (5, 1), (2026, 1)])
+def test_oracle_matches_reference_core_frameskip4(rom_seed, prg_banks):
+    """40 frame-skip-4 steps, full state after each; the 1-bank cases run the
+    16 KB (NROM-128) image mirrored at $8000 and $C000 (rom.cpp:65-121,
+    batch_bus.cuh:24-33), with vectors into the low copy."""
+    rom = synthrom.make_rom(rom_seed, prg_banks).rom
     o, r = O.Oracle(rom), O.RefConsole(rom)
     for k in range(40):
         m = int(synthrom.action_masks(rom_seed, 1, k)[0])
