@@ -37,8 +37,9 @@ frames/s and the useful-lane fraction, for 4,096 and 65,536 consoles.
 Resets while timed: each console's first episode starts at a seeded point of
 its level's done countdown, so the timed window holds the steady auto-reset
 rate; the dones of the timed steps are summed on the device and reported.
-``reset_burst_65536`` times single steps in which a whole level, or every
-console, auto-resets, against quiet steps.
+``reset_burst_65536`` times the same step with and without auto-reset on
+two batches in the same state: a step of the workload, and burst steps in
+which a whole level, or every console, ends its episode.
 
 ``cpu_baseline``: the reference's own CPU core (``nesle::Console`` compiled
 from the reference sources into oracle/_ref) on the host's cores (the job's
@@ -225,54 +226,62 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
 
 
 def run_reset_burst(core, rom: bytes, snapshots: list[bytes], levels: np.ndarray, done_vals: list[int],
-                    steps: int = 6) -> dict:
-    """Kernel time of single steps (HIP events, one step per timing window)
-    at 65,536 consoles: quiet steps (no console done), a burst step in which
-    every console of level 0 (1/8 of the batch) auto-resets, and one in which
-    every console does.  The ROM decrements the done byte in the NMI of every
-    frame whose incremented frame counter is a multiple of 8, so poking the
-    frame counter to 7 and the done byte to 1 makes the selected consoles
-    done in the first frame of the next step (the others get 200)."""
+                    done_init: np.ndarray, warmup: int = 40) -> dict:
+    """What auto-reset costs a step, at 65,536 consoles: two batches in the
+    same state take the same step, one with auto-reset and one without, and
+    their step-kernel times (HIP events, one step per timing window) differ
+    only by the resets.  Measured on a step of the benchmark workload itself
+    (after ``warmup`` steps), and on burst steps in which every console of
+    level 0 (1/8 of the batch), or every console, ends its episode: the ROM
+    decrements the done byte in the NMI of every frame whose incremented
+    frame counter is a multiple of 8, so poking the frame counter to 7 and
+    the done byte to 1 makes the selected consoles done in the first frame
+    of the next step (the others get 200)."""
     import torch
 
     n = levels.size
-    batch = core.CudaBatch(n, 4, rom, snapshots, levels, reward=reward_spec())
-    batch.set_stream(torch.cuda.current_stream().cuda_stream)
-    table = torch.from_numpy(synthrom.action_table(ACTION_SEED, n, 3 * steps + 4)).cuda()
-    dones = torch.from_dlpack(batch.last_done_device())
-    k = 0
-
-    def timed_step() -> tuple[float, int]:
-        nonlocal k
-        batch.set_timing(True)
-        batch.step_device(table[k], auto_reset=True, synchronize=False)
-        torch.cuda.synchronize()
-        ms, _ = batch.kernel_timing()
-        batch.set_timing(False)
-        k += 1
-        return ms, int(dones.to(torch.int64).sum().item())
-
+    pair = []
     for _ in range(2):
-        timed_step()
-    quiet = [timed_step() for _ in range(steps)]
-    assert all(d == 0 for _, d in quiet), "quiet steps ended episodes"
-    out = {"num_envs": n, "quiet_ms": [m for m, _ in quiet]}
+        b = core.CudaBatch(n, 4, rom, snapshots, levels, reward=reward_spec())
+        b.poke_ram_envs(synthrom.DONE_BYTE, done_init)
+        b.set_stream(torch.cuda.current_stream().cuda_stream)
+        pair.append(b)
+    table = torch.from_numpy(synthrom.action_table(ACTION_SEED, n, warmup + 8)).cuda()
+    for k in range(warmup):
+        for b in pair:
+            b.step_device(table[k], auto_reset=True, synchronize=False)
+    torch.cuda.synchronize()
+    k = warmup
+
+    def step_both() -> tuple[float, float, int]:
+        """(ms with auto-reset, ms without, dones) of the same step; the
+        batch without auto-reset then takes the same masked reset."""
+        nonlocal k
+        ms = []
+        for b, ar in zip(pair, (True, False)):
+            b.set_timing(True)
+            b.step_device(table[k], auto_reset=ar, synchronize=False)
+            torch.cuda.synchronize()
+            ms.append(b.kernel_timing()[0])
+            b.set_timing(False)
+        dones = torch.from_dlpack(pair[1].last_done_device()).clone()
+        pair[1].reset_envs_device(dones)
+        k += 1
+        return ms[0], ms[1], int(dones.to(torch.int64).sum().item())
+
+    out = {"num_envs": n, "warmup_steps": warmup}
+    steady = [step_both() for _ in range(3)]
+    out["workload_steps"] = [{"with_reset_ms": a, "without_ms": w, "dones": d} for a, w, d in steady]
     for name, sel in (("level0", levels == 0), ("all", np.ones(n, dtype=bool))):
         vals = np.full(n, 200, dtype=np.uint8)
         vals[sel] = 1
-        batch.poke_ram(synthrom.FRAME_COUNTER, 7)
-        batch.poke_ram_envs(synthrom.DONE_BYTE, vals)
-        ms, d = timed_step()
+        for b in pair:
+            b.poke_ram(synthrom.FRAME_COUNTER, 7)
+            b.poke_ram_envs(synthrom.DONE_BYTE, vals)
+        a, w, d = step_both()
         assert d == int(sel.sum()), f"burst {name}: {d} dones, expected {int(sel.sum())}"
-        after, d2 = timed_step()
-        assert d2 == 0, f"step after burst {name} ended episodes"
-        out[f"burst_{name}_ms"] = ms
-        out[f"burst_{name}_dones"] = d
-        out[f"after_burst_{name}_ms"] = after
-    q = float(np.median(out["quiet_ms"]))
-    out["quiet_median_ms"] = q
-    out["burst_level0_over_quiet"] = out["burst_level0_ms"] / q
-    out["burst_all_over_quiet"] = out["burst_all_ms"] / q
+        out[f"burst_{name}"] = {"with_reset_ms": a, "without_ms": w, "dones": d, "ratio": a / w}
+    out["workload_ratio"] = float(np.mean([a / w for a, w, _ in steady]))
     return out
 
 
@@ -457,9 +466,9 @@ def main() -> int:
     burst = None
     if args.burst:
         log("reset bursts: single-step kernel times")
-        burst = run_reset_burst(core, rom, snaps, levels, done_vals)
-        log(f"  quiet {burst['quiet_median_ms']:.2f} ms, level burst {burst['burst_level0_ms']:.2f} ms, "
-            f"all {burst['burst_all_ms']:.2f} ms")
+        burst = run_reset_burst(core, rom, snaps, levels, done_vals, done_init)
+        log(f"  step with/without auto-reset: workload x{burst['workload_ratio']:.4f}, level burst "
+            f"x{burst['burst_level0']['ratio']:.4f}, every console x{burst['burst_all']['ratio']:.4f}")
     log(f"timing {args.small_envs} envs x {args.small_steps} steps (no resets)")
     small = run_gpu(core, rom, args.small_envs, args.small_steps, max(5, args.warmup // 4), None, None)
     log(f"  {small['env_steps_per_s']:.0f} env-steps/s")

@@ -99,8 +99,49 @@ __device__ __forceinline__ void zero16(std::uint8_t* dst, std::uint32_t bytes) {
     for (std::uint32_t i = 0; i < bytes / 16; ++i) reinterpret_cast<uint4*>(dst)[i] = make_uint4(0, 0, 0, 0);
 }
 
-// Load a canonical blob into console `env` (all fields, arrays included).
-__device__ inline void load_blob(const DeviceState& s, std::uint32_t env, const std::uint8_t* b) {
+// Byte `k` (a compile-time index after unrolling) of a run of dwords.
+__device__ __forceinline__ std::uint32_t byte_at(const std::uint32_t* w, std::uint32_t k) {
+    return (w[k >> 2] >> (8 * (k & 3))) & 0xFF;
+}
+
+// `rows` bytes of a blob (16-byte aligned, rows a multiple of 16) into
+// consecutive rows of an address-major array at `dst` (= array + row0 *
+// pitch + env).  The blob is read 16 bytes at a time, four loads ahead of
+// the stores, so the copy waits on about one load round trip in all; the
+// byte stores are independent of each other.
+__device__ __forceinline__ void blob_rows(std::uint8_t* dst, std::uint32_t pitch, const std::uint8_t* src,
+                                          std::uint32_t rows) {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    const std::uint32_t chunks = rows / 16;
+    const std::uint32_t last = chunks - 1;
+    uint4 q0 = s4[0], q1 = s4[1 < last ? 1 : last], q2 = s4[2 < last ? 2 : last], q3 = s4[3 < last ? 3 : last];
+    std::uint32_t at = 0;
+#pragma unroll 1
+    for (std::uint32_t c = 0; c < chunks; ++c) {
+        const std::uint32_t w[4] = {q0.x, q0.y, q0.z, q0.w};
+        q0 = q1;
+        q1 = q2;
+        q2 = q3;
+        q3 = s4[c + 4 < last ? c + 4 : last];
+#pragma unroll
+        for (std::uint32_t k = 0; k < 16; ++k) {
+            dst[at] = static_cast<std::uint8_t>(byte_at(w, k));
+            at += pitch;
+        }
+    }
+}
+
+__device__ __forceinline__ void zero_rows(std::uint8_t* dst, std::uint32_t pitch, std::uint32_t rows) {
+    std::uint32_t at = 0;
+#pragma unroll 16
+    for (std::uint32_t r = 0; r < rows; ++r) {
+        dst[at] = 0;
+        at += pitch;
+    }
+}
+
+// The scalar fields and $4000-$4017 of a canonical blob into console `env`.
+__device__ inline void blob_scalars(const DeviceState& s, std::uint32_t env, const std::uint8_t* b) {
     using namespace blob;
     s.pc[env] = static_cast<std::uint16_t>(le16(b, kPc));
     s.a[env] = b[kA]; s.x[env] = b[kX]; s.y[env] = b[kY]; s.sp[env] = b[kSp]; s.p[env] = b[kP];
@@ -114,22 +155,15 @@ __device__ inline void load_blob(const DeviceState& s, std::uint32_t env, const 
     s.fine_x[env] = b[kFineX]; s.w[env] = b[kW]; s.scroll_x[env] = b[kScrollX]; s.scroll_y[env] = b[kScrollY];
     s.c1_buttons[env] = b[kC1Buttons]; s.c1_shift[env] = b[kC1Shift]; s.c1_count[env] = b[kC1Count];
     s.strobe[env] = b[kStrobe]; s.c2_count[env] = b[kC2Count]; s.fault[env] = b[kFault];
-    const std::size_t pitch = s.pitch;
-    for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * pitch + env] = b[kApuIo + i];
-    for (std::uint32_t i = 0; i < kRamBytes; ++i) s.ram[i * pitch + env] = b[kRam + i];
-    for (std::uint32_t i = 0; i < kPrgRamBytes; ++i) s.prg_ram[i * pitch + env] = b[kPrgRam + i];
-    std::uint8_t* vm = vram_of(s, env);
-    copy16(vm + vram::kOam, b + kOam, kOamBytes);
-    copy16(vm + vram::kPalette, b + kPalette, kPaletteBytes);
-    copy16(vm + vram::kNametable, b + kNametable, s.nt_bytes);
-    if (s.chr_ram != nullptr)
-        for (std::uint32_t i = 0; i < kChrRamBytes; ++i) s.chr_ram[i * pitch + env] = b[kChrRam + i];
+    for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * s.pitch + env] = b[kApuIo + i];
 }
 
-// Power-on state: the reference CPU core after construction + reset_cpu
-// (console.hpp:38-47,103-106; cpu.hpp:84-92); identical to the reference's
-// cold reset of a batched console (batch_step.cuh:109-172).
-__device__ inline void cold_reset(const DeviceState& s, std::uint32_t env, const std::uint8_t* prg) {
+// Power-on scalars: the reference CPU core after construction + reset_cpu
+// (console.hpp:38-47,103-106; cpu.hpp:84-92), identical to the reference's
+// cold reset of a batched console (batch_step.cuh:109-172); every array of
+// the console is zero at power-on.
+__device__ inline void power_on_scalars(const DeviceState& s, std::uint32_t env) {
+    const std::uint8_t* prg = s.prg_rom;
     s.pc[env] = static_cast<std::uint16_t>(prg[0xFFFC & s.prg_mask] | (prg[0xFFFD & s.prg_mask] << 8));
     s.a[env] = 0; s.x[env] = 0; s.y[env] = 0; s.sp[env] = 0xFD; s.p[env] = 0x24;
     s.nmi_pending[env] = 0; s.cycles[env] = 7; s.frame[env] = 0; s.frame_dot[env] = 0;
@@ -138,28 +172,7 @@ __device__ inline void cold_reset(const DeviceState& s, std::uint32_t env, const
     s.scroll_x[env] = 0; s.scroll_y[env] = 0;
     s.c1_buttons[env] = 0; s.c1_shift[env] = 0; s.c1_count[env] = 8; s.strobe[env] = 0; s.c2_count[env] = 8;
     s.fault[env] = 0;
-    const std::size_t pitch = s.pitch;
-    for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * pitch + env] = 0;
-    for (std::uint32_t i = 0; i < kRamBytes; ++i) s.ram[i * pitch + env] = 0;
-    for (std::uint32_t i = 0; i < kPrgRamBytes; ++i) s.prg_ram[i * pitch + env] = 0;
-    zero16(vram_of(s, env), s.vram_stride);
-    if (s.chr_ram != nullptr)
-        for (std::uint32_t i = 0; i < kChrRamBytes; ++i) s.chr_ram[i * pitch + env] = 0;
-}
-
-// Rewards/dones of the terminal step stay visible after the reset, as the
-// reference's last_rewards/last_done copies do (cuda_module.cu:635-656).
-__device__ __forceinline__ void reset_env(const DeviceState& s, std::uint32_t env, const std::uint8_t* prg) {
-    if (s.bank != nullptr) {
-        load_blob(s, env, s.bank + static_cast<std::size_t>(s.env_to_level[env]) * blob::kBytes);
-    } else {
-        cold_reset(s, env, prg);
-    }
-}
-
-// Reward baselines from the console's current RAM (in HBM).
-__device__ inline void seed_baselines(const DeviceState& s, std::uint32_t env) {
-    reward_seed(s, env, GlobalRam{s, env});
+    for (std::uint32_t i = 0; i < kApuIoBytes; ++i) s.apu_io[i * s.pitch + env] = 0;
 }
 
 }  // namespace nesle

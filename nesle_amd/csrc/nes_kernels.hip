@@ -1,6 +1,7 @@
-// nes_kernels.hip -- utility kernels of libnesle_hip.so: masked reset from
-// the snapshot bank or power-on (the reference's reset kernels,
-// cpp/src/cuda/kernels.cu:177-203), full-state save/load of one console,
+// nes_kernels.hip -- utility kernels of libnesle_hip.so: masked restore of
+// consoles from the snapshot bank, from one blob, or to power-on (the
+// reference's reset kernels, cpp/src/cuda/kernels.cu:177-203, and the
+// auto-reset that follows a step), full-state save of one console,
 // the env-major RAM observation, int64 action ingestion
 // (cpp/bindings/cuda_module.cu:310-317) and RAM poke (cuda_module.cu:356-364).
 // The console step kernel lives in nes_step.hip.
@@ -17,21 +18,87 @@ namespace {
 
 constexpr std::uint32_t kBlock = 256;
 
-// Masked reset: snapshot bank when present, else power-on.
-__global__ void __launch_bounds__(kBlock) reset_kernel(DeviceState s, const std::uint8_t* mask) {
-    const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
-    if (env >= s.n || (mask != nullptr && mask[env] == 0)) return;
-    reset_env(s, env, s.prg_rom);
-    seed_baselines(s, env);
-}
+// Masked restore, tiled for the address-major layout: blockIdx.x picks 64
+// consecutive consoles (one wave, lane = console), blockIdx.y one share of
+// the work — a run of kRestoreRows interleaved RAM/PRG-RAM rows, a run of
+// CHR-RAM rows, or (the last y) the scalars, video memory and reward
+// baselines.  A tile without a selected console leaves at once.  The
+// consoles' sources are the bank slot of their level, one fixed blob, or
+// power-on zeros; the baselines are seeded from the source blob's RAM, so
+// no block reads rows another block writes.  A restore of a few consoles
+// thus costs about one row run's byte stores, spread over many waves.
+constexpr std::uint32_t kRestoreRows = 512;
+constexpr std::uint32_t kRamRowBlocks = (kRamBytes + kPrgRamBytes) / kRestoreRows;   // 20
+constexpr std::uint32_t kChrRowBlocks = kChrRamBytes / kRestoreRows;                  // 16
 
-// Load one blob into every console selected by mask (null = all).
-__global__ void __launch_bounds__(kBlock) load_blob_kernel(DeviceState s, const std::uint8_t* blob_src,
-                                                           const std::uint8_t* mask) {
-    const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
-    if (env >= s.n || (mask != nullptr && mask[env] == 0)) return;
-    load_blob(s, env, blob_src);
-    seed_baselines(s, env);
+__global__ void __launch_bounds__(64) restore_kernel(DeviceState s, const std::uint8_t* mask,
+                                                     const std::uint8_t* fixed_blob) {
+    const std::uint32_t env = blockIdx.x * 64 + threadIdx.x;
+    const bool mine = env < s.n && (mask == nullptr || mask[env] != 0);
+    if (__ballot(mine) == 0) return;
+    // Source of console e: the fixed blob, its level's bank slot, or null
+    // (power-on).
+    auto source = [&](std::uint32_t e) -> const std::uint8_t* {
+        if (fixed_blob != nullptr) return fixed_blob;
+        if (s.bank == nullptr) return nullptr;
+        return s.bank + static_cast<std::size_t>(s.env_to_level[e]) * blob::kBytes;
+    };
+    const std::uint8_t* src = mine ? source(env) : nullptr;
+    const std::uint32_t y = blockIdx.y, pitch = s.pitch;
+    if (y < kRamRowBlocks) {
+        if (!mine) return;
+        std::uint8_t* dst = s.ram + static_cast<std::size_t>(y * kRestoreRows) * pitch + env;
+        if (src != nullptr) {
+            blob_rows(dst, pitch, src + blob::kRam + y * kRestoreRows, kRestoreRows);
+        } else {
+            zero_rows(dst, pitch, kRestoreRows);
+        }
+        return;
+    }
+    if (y < kRamRowBlocks + kChrRowBlocks) {
+        if (!mine || s.chr_ram == nullptr) return;
+        const std::uint32_t r0 = (y - kRamRowBlocks) * kRestoreRows;
+        std::uint8_t* dst = s.chr_ram + static_cast<std::size_t>(r0) * pitch + env;
+        if (src != nullptr) {
+            blob_rows(dst, pitch, src + blob::kChrRam + r0, kRestoreRows);
+        } else {
+            zero_rows(dst, pitch, kRestoreRows);
+        }
+        return;
+    }
+    // Scalars and baselines per console; video memory by the whole wave, one
+    // selected console at a time (contiguous 16-byte runs).
+    if (mine) {
+        if (src != nullptr) {
+            blob_scalars(s, env, src);
+            reward_seed(s, env, [&](std::uint32_t a) -> std::uint32_t { return src[blob::kRam + (a & 0x7FF)]; });
+        } else {
+            power_on_scalars(s, env);
+            reward_seed(s, env, [](std::uint32_t) -> std::uint32_t { return 0; });
+        }
+    }
+    const std::uint32_t lane = threadIdx.x;
+    std::uint64_t todo = __ballot(mine);
+    while (todo != 0) {
+        const std::uint32_t k = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(todo)) - 1);
+        todo &= todo - 1;
+        const std::uint32_t e = blockIdx.x * 64 + k;   // wave-uniform
+        const std::uint8_t* from = source(e);
+        uint4* vm = reinterpret_cast<uint4*>(vram_of(s, e));
+        // Video memory block: palette (2 x 16 B), OAM (16), nametables (128 or 256).
+        const std::uint32_t words = s.vram_stride / 16;
+        for (std::uint32_t i = lane; i < words; i += 64) {
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (from != nullptr) {
+                const std::uint32_t o = 16 * i;
+                const std::uint32_t at = o < vram::kOam ? blob::kPalette + o
+                                       : o < vram::kNametable ? blob::kOam + (o - vram::kOam)
+                                                              : blob::kNametable + (o - vram::kNametable);
+                v = *reinterpret_cast<const uint4*>(from + at);
+            }
+            vm[i] = v;
+        }
+    }
 }
 
 // Gather console `env` into a canonical blob, one byte per thread.
@@ -125,7 +192,7 @@ __global__ void __launch_bounds__(kBlock) poke_ram_envs_kernel(DeviceState s, st
 
 __global__ void __launch_bounds__(kBlock) seed_kernel(DeviceState s) {
     const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
-    if (env < s.n) seed_baselines(s, env);
+    if (env < s.n) reward_seed(s, env, GlobalRam{s, env});
 }
 
 // Presentation snapshot from live state, so a render right after a reset or
@@ -157,15 +224,20 @@ inline std::uint32_t blocks_for(std::uint32_t n) { return (n + kBlock - 1) / kBl
 
 }  // namespace
 
-hipError_t launch_reset(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream) {
-    reset_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, mask);
+hipError_t launch_restore(const DeviceState& s, const std::uint8_t* mask, const std::uint8_t* fixed_blob,
+                          hipStream_t stream) {
+    const dim3 grid((s.n + 63) / 64, kRamRowBlocks + kChrRowBlocks + 1);
+    restore_kernel<<<grid, dim3(64), 0, stream>>>(s, mask, fixed_blob);
     return hipGetLastError();
+}
+
+hipError_t launch_reset(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream) {
+    return launch_restore(s, mask, nullptr, stream);
 }
 
 hipError_t launch_load_blob(const DeviceState& s, const std::uint8_t* blob_src, const std::uint8_t* mask,
                             hipStream_t stream) {
-    load_blob_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, blob_src, mask);
-    return hipGetLastError();
+    return launch_restore(s, mask, blob_src, stream);
 }
 
 hipError_t launch_save_blob(const DeviceState& s, std::uint32_t env, std::uint8_t* out, hipStream_t stream) {

@@ -15,6 +15,8 @@ namespace nesle {
 hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr,
                        bool auto_reset, int stats_mode, hipStream_t stream);
 // Masked (null = all) reset from the snapshot bank, or power-on without one.
+// The fused auto-reset of a step is this launch with the step's done flags
+// as the mask.
 hipError_t launch_reset(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
 hipError_t launch_load_blob(const DeviceState& s, const std::uint8_t* blob_src, const std::uint8_t* mask,
                             hipStream_t stream);

@@ -2,8 +2,11 @@
 //
 // One lane per console.  Per launch a lane runs `frameskip` NES frames: NMI
 // entry, the 6502 instruction, OAM DMA, lazy PPU settlement at the timing
-// events, then the reward/done rule and, if asked, a fused auto-reset from the
-// snapshot bank.  Semantics follow the reference's CPU core
+// events, then the reward/done rule.  The auto-reset of done consoles is the
+// restore kernel (nes_kernels.hip) launched right after on the same stream:
+// kept out of this kernel, its code cannot change how the main loop is
+// compiled, and it spreads a reset over many waves instead of one lane's
+// serial copy.  Semantics follow the reference's CPU core
 // (cpp/include/nesle/console.hpp:49-150, cpu.hpp:84-730, ppu.hpp:46-395,
 // controller.hpp:18-67); the launch mirrors the reference's console_step_kernel
 // (cpp/src/cuda/kernels.cu:19-104) and its snapshot reset (kernels.cu:195-203).
@@ -445,7 +448,7 @@ struct Console {
 // bound of the 8- and 16-wave workgroups (with the tighter one it is 3 % slower).
 template <int kStats, bool kFull, bool kBudget>
 __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceState s, std::uint32_t frameskip, std::uint32_t max_instr,
-                                                         std::uint32_t auto_reset, std::uint32_t lane_bits) {
+                                                         std::uint32_t lane_bits) {
     using C = Console<kFull>;
     const std::uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, T = blockDim.x;
     const std::uint32_t L = 1u << lane_bits;
@@ -900,10 +903,6 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         s.stat_frames[env] = frames;
         s.stat_budget_hits[env] = c.r32(reg::kBudgetHits);
     }
-    if (auto_reset && done) {
-        reset_env(s, env, lds);
-        seed_baselines(s, env);
-    }
 }
 
 struct Geometry {
@@ -929,17 +928,17 @@ Geometry geometry(std::uint32_t n, std::uint32_t waves) {
 
 template <int kStats, bool kFull, bool kBudget>
 hipError_t launch_variant(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
-                          std::uint32_t auto_reset, hipStream_t stream) {
+                          hipStream_t stream) {
     step_kernel<kStats, kFull, kBudget><<<dim3(g.blocks), dim3(64 * g.waves), 0, stream>>>(
-        s, frameskip, max_instr, auto_reset, g.lane_bits);
+        s, frameskip, max_instr, g.lane_bits);
     return hipGetLastError();
 }
 
 template <int kStats, bool kBudget>
 hipError_t launch_mode(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
-                       std::uint32_t auto_reset, hipStream_t stream) {
-    return g.full ? launch_variant<kStats, true, kBudget>(s, g, frameskip, max_instr, auto_reset, stream)
-                  : launch_variant<kStats, false, kBudget>(s, g, frameskip, max_instr, auto_reset, stream);
+                       hipStream_t stream) {
+    return g.full ? launch_variant<kStats, true, kBudget>(s, g, frameskip, max_instr, stream)
+                  : launch_variant<kStats, false, kBudget>(s, g, frameskip, max_instr, stream);
 }
 
 // Waves per workgroup: NESLE_WAVES_PER_GROUP (4, 8 or 16) overrides the default.
@@ -958,13 +957,22 @@ hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint3
                        int stats_mode, hipStream_t stream) {
     Geometry g = geometry(s.n, waves_per_group());
     if (g.full && g.waves != 4) g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
-    const std::uint32_t ar = auto_reset ? 1u : 0u;
     // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
     const bool budget = max_instr < 15000;
-    if (stats_mode == 2) return launch_mode<2, true>(s, g, frameskip, max_instr, ar, stream);
-    if (stats_mode == 1) return launch_mode<1, true>(s, g, frameskip, max_instr, ar, stream);
-    return budget ? launch_mode<0, true>(s, g, frameskip, max_instr, ar, stream)
-                  : launch_mode<0, false>(s, g, frameskip, max_instr, ar, stream);
+    hipError_t e;
+    if (stats_mode == 2) {
+        e = launch_mode<2, true>(s, g, frameskip, max_instr, stream);
+    } else if (stats_mode == 1) {
+        e = launch_mode<1, true>(s, g, frameskip, max_instr, stream);
+    } else {
+        e = budget ? launch_mode<0, true>(s, g, frameskip, max_instr, stream)
+                   : launch_mode<0, false>(s, g, frameskip, max_instr, stream);
+    }
+    if (e != hipSuccess || !auto_reset) return e;
+    // Auto-reset: done consoles restored from their level's snapshot (or
+    // powered on); rewards and dones of the step stay as written, as the
+    // reference's last_rewards/last_done copies do (cuda_module.cu:635-656).
+    return launch_reset(s, s.done, stream);
 }
 
 }  // namespace nesle
