@@ -17,6 +17,8 @@ extern "C" {
 #endif
 
 #define NESLE_PPO_MAX_ACTIONS 1024u
+/* Largest minibatch nesle_ppo_head_static takes (its static scratch). */
+#define NESLE_PPO_STATIC_MAX_BATCH 1048576u
 
 /* Floats of scratch nesle_ppo_head needs for a minibatch of `batch` rows. */
 uint32_t nesle_ppo_head_scratch_floats(uint32_t batch);
@@ -44,6 +46,21 @@ int nesle_ppo_head(const float* logits, const float* value, const int64_t* actio
                    const float* advantages, const float* returns, uint32_t batch, uint32_t num_actions,
                    double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
                    float* scratch, float* loss, float* clipfrac, float* accum, void* stream);
+
+/* nesle_ppo_head without the scratch argument: the same kernels on a
+ * library-owned scratch array of static device storage (64 KiB per device,
+ * held until the process ends), so the call allocates nothing.  No
+ * counterpart in the reference: for callers that cannot allocate or be
+ * handed a workspace, such as code under HIP graph capture or a serving
+ * loop that forbids allocation.  The current device must be the one the
+ * pointers and the stream belong to.  Every call on a device shares that
+ * device's scratch: calls that overlap on one GPU (other streams, other
+ * threads) race; calls in order on one stream do not.  Fails with
+ * NESLE_EINVAL as nesle_ppo_head, and for batch > NESLE_PPO_STATIC_MAX_BATCH. */
+int nesle_ppo_head_static(const float* logits, const float* value, const int64_t* actions, const float* old_logprob,
+                          const float* advantages, const float* returns, uint32_t batch, uint32_t num_actions,
+                          double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
+                          float* loss, float* clipfrac, float* accum, void* stream);
 
 #ifdef __cplusplus
 }

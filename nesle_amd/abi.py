@@ -137,6 +137,9 @@ def lib():
         "nesle_ppo_head_scratch_floats": (ctypes.c_uint32, [ctypes.c_uint32]),
         "nesle_ppo_head": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double,
                                           ctypes.c_double, ctypes.c_double, vp, vp, vp, vp, vp, vp, vp]),
+        "nesle_ppo_head_static": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32,
+                                                 ctypes.c_double, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp,
+                                                 vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -21,8 +21,10 @@
 // [lo, hi], bounds included.
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "nes_launch.h"
@@ -156,45 +158,124 @@ __global__ void __launch_bounds__(kStats) head_final(const float* partials, std:
     }
 }
 
-}  // namespace
+std::uint32_t scratch_floats(std::uint32_t batch) { return 2u + 4u * ((batch + kRows - 1) / kRows); }
 
-extern "C" {
+constexpr std::uint32_t kStaticScratchFloats = 2u + 4u * ((NESLE_PPO_STATIC_MAX_BATCH + kRows - 1) / kRows);
 
-std::uint32_t nesle_ppo_head_scratch_floats(std::uint32_t batch) {
-    return 2u + 4u * ((batch + kRows - 1) / kRows);
-}
+// Device address of `scratch` (defined below) on each device, looked up on
+// the first call made with that device current (the array's name in host
+// code is only a stand-in for the symbol).
+constexpr int kMaxDevices = 64;
+std::array<float*, kMaxDevices> g_scratch_ptr{};
+std::mutex g_scratch_mu;
 
-int nesle_ppo_head(const float* logits, const float* value, const std::int64_t* actions, const float* old_logprob,
-                   const float* advantages, const float* returns, std::uint32_t batch, std::uint32_t num_actions,
-                   double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
-                   float* scratch, float* loss, float* clipfrac, float* accum, void* stream) {
+int check_args(const char* who, const float* logits, const float* value, const std::int64_t* actions,
+               const float* old_logprob, const float* advantages, const float* returns, std::uint32_t batch,
+               std::uint32_t num_actions, const float* dlogits, const float* dvalue, const float* loss,
+               const float* clipfrac) {
     if (batch == 0 || num_actions == 0 || num_actions > NESLE_PPO_MAX_ACTIONS) {
-        nesle::set_last_error("nesle_ppo_head: batch must be >= 1 and num_actions in 1.." +
+        nesle::set_last_error(std::string(who) + ": batch must be >= 1 and num_actions in 1.." +
                               std::to_string(NESLE_PPO_MAX_ACTIONS));
         return NESLE_EINVAL;
     }
-    if (!logits || !value || !actions || !old_logprob || !advantages || !returns || !dlogits || !dvalue ||
-        !scratch || !loss || !clipfrac) {
-        nesle::set_last_error("nesle_ppo_head: null device pointer");
+    if (!logits || !value || !actions || !old_logprob || !advantages || !returns || !dlogits || !dvalue || !loss ||
+        !clipfrac) {
+        nesle::set_last_error(std::string(who) + ": null device pointer");
         return NESLE_EINVAL;
     }
+    return NESLE_OK;
+}
+
+int launch_head(const char* who, const float* logits, const float* value, const std::int64_t* actions,
+                const float* old_logprob, const float* advantages, const float* returns, std::uint32_t batch,
+                std::uint32_t num_actions, double clip_coef, double ent_coef, double vf_coef, float* dlogits,
+                float* dvalue, float* scratch_buf, float* loss, float* clipfrac, float* accum, void* stream) {
     const auto s = static_cast<hipStream_t>(stream);
     const std::uint32_t blocks = (batch + kRows - 1) / kRows;
     const float inv_n = 1.0f / static_cast<float>(batch);
     HeadArgs h{logits, value, actions, old_logprob, advantages, returns, batch, num_actions,
                static_cast<float>(1.0 - clip_coef), static_cast<float>(1.0 + clip_coef), static_cast<float>(clip_coef),
                static_cast<float>(ent_coef) * inv_n, static_cast<float>(vf_coef) * inv_n, inv_n,
-               scratch, dlogits, dvalue, scratch + 2};
-    hipLaunchKernelGGL(adv_stats, dim3(1), dim3(kStats), 0, s, advantages, batch, scratch);
+               scratch_buf, dlogits, dvalue, scratch_buf + 2};
+    hipLaunchKernelGGL(adv_stats, dim3(1), dim3(kStats), 0, s, advantages, batch, scratch_buf);
     hipLaunchKernelGGL(head_rows, dim3(blocks), dim3(kRows), 0, s, h);
-    hipLaunchKernelGGL(head_final, dim3(1), dim3(kStats), 0, s, scratch + 2, blocks, inv_n,
+    hipLaunchKernelGGL(head_final, dim3(1), dim3(kStats), 0, s, scratch_buf + 2, blocks, inv_n,
                        static_cast<float>(ent_coef), static_cast<float>(vf_coef), loss, clipfrac, accum);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
-        nesle::set_last_error(std::string("nesle_ppo_head: launch failed: ") + hipGetErrorString(e));
+        nesle::set_last_error(std::string(who) + ": launch failed: " + hipGetErrorString(e));
         return NESLE_EDEVICE;
     }
     return NESLE_OK;
+}
+
+}  // namespace
+
+// Scratch of the allocation-free entry point: the advantage statistics (2
+// floats) and the per-workgroup partial sums (4 floats per 256 rows) of
+// minibatches up to NESLE_PPO_STATIC_MAX_BATCH rows, about 64 KiB per
+// device.  Every call writes all of the scratch it reads before reading it,
+// so nothing needs clearing between calls.
+static __device__ __align__(256) float scratch[kStaticScratchFloats];
+
+extern "C" {
+
+std::uint32_t nesle_ppo_head_scratch_floats(std::uint32_t batch) { return scratch_floats(batch); }
+
+int nesle_ppo_head(const float* logits, const float* value, const std::int64_t* actions, const float* old_logprob,
+                   const float* advantages, const float* returns, std::uint32_t batch, std::uint32_t num_actions,
+                   double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
+                   float* scratch_buf, float* loss, float* clipfrac, float* accum, void* stream) {
+    const int rc = check_args("nesle_ppo_head", logits, value, actions, old_logprob, advantages, returns, batch,
+                              num_actions, dlogits, dvalue, loss, clipfrac);
+    if (rc != NESLE_OK) return rc;
+    if (scratch_buf == nullptr) {
+        nesle::set_last_error("nesle_ppo_head: null device pointer");
+        return NESLE_EINVAL;
+    }
+    return launch_head("nesle_ppo_head", logits, value, actions, old_logprob, advantages, returns, batch,
+                       num_actions, clip_coef, ent_coef, vf_coef, dlogits, dvalue, scratch_buf, loss, clipfrac,
+                       accum, stream);
+}
+
+int nesle_ppo_head_static(const float* logits, const float* value, const std::int64_t* actions,
+                          const float* old_logprob, const float* advantages, const float* returns, std::uint32_t batch,
+                          std::uint32_t num_actions, double clip_coef, double ent_coef, double vf_coef,
+                          float* dlogits, float* dvalue, float* loss, float* clipfrac, float* accum, void* stream) {
+    const char* who = "nesle_ppo_head_static";
+    const int rc = check_args(who, logits, value, actions, old_logprob, advantages, returns, batch, num_actions,
+                              dlogits, dvalue, loss, clipfrac);
+    if (rc != NESLE_OK) return rc;
+    if (batch > NESLE_PPO_STATIC_MAX_BATCH) {
+        nesle::set_last_error(std::string(who) + ": batch " + std::to_string(batch) + " exceeds the static scratch (" +
+                              std::to_string(NESLE_PPO_STATIC_MAX_BATCH) + " rows); use nesle_ppo_head with a workspace");
+        return NESLE_EINVAL;
+    }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        nesle::set_last_error(std::string(who) + ": no usable current device" +
+                              (e != hipSuccess ? std::string(": ") + hipGetErrorString(e) : std::string()));
+        return NESLE_EDEVICE;
+    }
+    float* ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_ptr[dev];
+        if (ptr == nullptr) {
+            void* addr = nullptr;
+            e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || addr == nullptr) {
+                nesle::set_last_error(std::string(who) + ": hipGetSymbolAddress(scratch) failed: " +
+                                      hipGetErrorString(e));
+                return NESLE_EDEVICE;
+            }
+            ptr = static_cast<float*>(addr);
+            g_scratch_ptr[dev] = ptr;
+        }
+    }
+    return launch_head(who, logits, value, actions, old_logprob, advantages, returns, batch, num_actions, clip_coef,
+                       ent_coef, vf_coef, dlogits, dvalue, ptr, loss, clipfrac, accum, stream);
 }
 
 }  // extern "C"
