@@ -178,3 +178,20 @@ def test_frames_off_batch_refuses_render():
         b.view(abi.VIEW_FRAME_RGB)
     with pytest.raises(ValueError):
         abi.Batch(rom, 4, frameskip=4).render(0)
+
+
+def test_pixel_workload_full_size_sampled():
+    """The pixel-observation workload at its full size: 16,384 consoles,
+    frame-skip 4, an 84x84 gray frame of every console rendered after every
+    step; sampled consoles (wave, workgroup and range edges, random ones)
+    equal the oracle's batched-renderer frame turned gray, at every step."""
+    num_envs = 16384
+    rom = _rom(2026)
+    rng = np.random.default_rng(7)
+    sample = sorted({0, 1, 63, 64, 255, 256, 8191, 8192, num_envs - 1, *rng.integers(0, num_envs, 6).tolist()})
+    say(f"[gpu] pixel workload: N={num_envs} fs=4 sample={sample}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    oracles = {e: O.Oracle(rom) for e in sample}
+    for k in range(3):
+        _step_all(b, oracles, 0x5EED, k, 4)
+        _check(b, oracles, f"step {k}", abi.FRAME_GRAY84)

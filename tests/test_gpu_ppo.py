@@ -219,3 +219,52 @@ def test_ppo_head_matches_the_reference_loss_and_its_gradients(n, a, spread):
         torch.testing.assert_close(gv.grad.cpu(), ref_v.grad, rtol=1e-4, atol=1e-7)
     if spread == 0.0:
         assert float(want_cf) == 0.0
+
+
+def test_ppo_update_at_full_size_sampled():
+    """One PPO update of the benchmark's configuration at full size: 8,192
+    consoles x 128 steps on 8 snapshot levels with the x-delta rule and
+    auto-reset, 12-way actions, Xavier init, GAE, 4 epochs of minibatch
+    8,192.  Sampled consoles' rewards and dones at every rollout step equal
+    oracle consoles fed the same controller masks (restoring their level's
+    snapshot after each done); the update changes every parameter."""
+    rom = synthrom.make_rom(2026).rom
+    say("[gpu] ppo full size: snapshot bank")
+    snaps = warm_snapshots(rom, [100, 180, 260, 340, 420, 500, 580, 660], seed=77)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 3 + 2 * i        # episodes of 24-136 frames
+    n, T = 8192, 128
+    levels = np.random.default_rng(78).integers(0, 8, n)
+    reward = dict(kind="x_delta", x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE,
+                  clip=15, time_penalty=0.01)
+    cfg = P.NativePPOConfig("synthetic.nes", num_envs=n, n_steps=T, batch_size=8192, update_epochs=4,
+                            frameskip=4, action_space="complex", init="xavier", reward=reward,
+                            total_timesteps=n * T, save_checkpoints=False, seed=1,
+                            env_to_level=tuple(int(x) for x in levels))
+    rng = np.random.default_rng(2)
+    sample = sorted({0, 1, 63, 64, 4095, 4096, n - 1, *rng.integers(0, n, 7).tolist()})
+    rec = []
+    say(f"[gpu] ppo full size: N={n} T={T} minibatch 8192 x 4 epochs, sample={sample}")
+    stats = P.train_native_ppo(cfg, rom_bytes=rom, snapshot_bytes=[bytes(s) for s in snaps],
+                               record=lambda k, m, r, d: rec.append((m[sample].cpu().numpy(),
+                                                                     r[sample].cpu().numpy().copy(),
+                                                                     d[sample].cpu().numpy().copy())))
+    assert stats["updates"] == 1 and len(rec) == T
+    assert math.isfinite(stats["log"][-1]["loss"])
+    ob = OracleBatch(rom, list(range(len(sample))), reward=dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                                                                done_addr=synthrom.DONE_BYTE, clip=15,
+                                                                time_penalty=0.01))
+    for j, c in enumerate(ob.cons):
+        c.load(snaps[levels[sample[j]]])
+    ends = 0
+    for k, (masks, rew, done) in enumerate(rec):
+        _, want_r, want_d = ob.step(masks, 4)
+        np.testing.assert_array_equal(rew, want_r, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(done, want_d.astype(bool), err_msg=f"step {k} dones")
+        for j in np.nonzero(want_d)[0]:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += int(want_d.sum())
+    assert ends >= len(sample)
+    torch.manual_seed(cfg.seed)
+    init = P._make_model(2048, 12, 256, "xavier", torch.device("cuda"))
+    assert all(not torch.equal(a, b) for a, b in zip(init.parameters(), stats["model"].parameters()))
