@@ -26,7 +26,10 @@
 //  * Registers A/X/Y/SP are packed in one VGPR; the microcode drives one
 //    branch-free datapath (addressing, stack window, next PC, ALU, flags).
 //    Finished lanes and NMI entry run as virtual opcodes, so nothing needs a
-//    commit select.  PPU and pad registers live in a per-console LDS area.
+//    commit select.  The registers that I/O reads touch ($2002, $4016/7:
+//    status, open bus, write toggle, pads) are packed into VGPRs, so those
+//    reads take no LDS round trip; the other PPU registers live in a
+//    per-console LDS area.
 //  * Only the HBM operand and the I/O register read branch inside the loop;
 //    everything rare (I/O writes, JMP indirect, stack wrap, idle loops,
 //    illegal opcodes, PPU events, OAM DMA, code outside ROM) sits behind one
@@ -81,6 +84,11 @@ constexpr std::uint32_t kBytes = 40;
 
 // Bits of a console's `flags` VGPR.
 constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4, kPresentPending = 8;
+// The PPU and pad registers every I/O read touches live in VGPRs: the write
+// toggle and pad strobe as `flags` bits, pad 1's buttons in `flags` bits
+// 8-15, and `io` = open bus (bits 0-7) | PPUSTATUS (8-15) | pad 1 shift
+// register (16-23) | pad 1 reads (24-27) | pad 2 reads (28-31).
+constexpr std::uint32_t kWToggle = 16, kStrobeBit = 32;
 
 // Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
 // write to (one spare byte per console after PRG RAM).
@@ -150,10 +158,26 @@ struct Console {
     const DeviceState& s;
     std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
-    // Hot state in VGPRs: CPU registers and `flags` (NMI latch, pending OAM
-    // DMA, fault).  PPU and pad registers live in the console's LDS register
-    // area (reg::*): only the I/O paths, PPU settlement and NMI entry touch them.
-    std::uint32_t pc, regs, p, flags;
+    // Hot state in VGPRs: CPU registers, `flags` (NMI latch, pending OAM DMA,
+    // fault, write toggle, strobe, pad 1 buttons) and `io` (open bus, status,
+    // pad shift state).  The other PPU registers live in the console's LDS
+    // register area (reg::*): only the I/O paths, PPU settlement and NMI entry
+    // touch them.
+    std::uint32_t pc, regs, p, flags, io;
+
+    // ---- VGPR-resident I/O registers ------------------------------------------------
+    __device__ __forceinline__ std::uint32_t open_bus() const { return io & 0xFF; }
+    __device__ __forceinline__ void set_open_bus(std::uint32_t v) { io = (io & ~0xFFu) | (v & 0xFF); }
+    __device__ __forceinline__ std::uint32_t status() const { return ubfe(io, 8, 8); }
+    __device__ __forceinline__ void set_status(std::uint32_t v) { io = (io & ~0xFF00u) | ((v & 0xFF) << 8); }
+    __device__ __forceinline__ std::uint32_t c1_shift() const { return ubfe(io, 16, 8); }
+    __device__ __forceinline__ std::uint32_t c1_count() const { return ubfe(io, 24, 4); }
+    __device__ __forceinline__ std::uint32_t c2_count() const { return io >> 28; }
+    __device__ __forceinline__ void set_c1(std::uint32_t shift, std::uint32_t count) {
+        io = (io & 0xF000FFFFu) | ((shift & 0xFF) << 16) | ((count & 0xF) << 24);
+    }
+    __device__ __forceinline__ void set_c2_count(std::uint32_t n) { io = (io & 0x0FFFFFFFu) | (n << 28); }
+    __device__ __forceinline__ std::uint32_t buttons() const { return ubfe(flags, 8, 8); }
 
     // ---- LDS register area ----------------------------------------------------------
     __device__ __forceinline__ std::uint32_t r8(std::uint32_t f) const { return lds[base + kRegs + f]; }
@@ -245,12 +269,9 @@ struct Console {
         if (addr < 0x4000) {
             const std::uint32_t reg = addr & 7;
             if (reg == 2) {
-                const std::uint32_t st = r8(reg::kStatus);
-                const std::uint32_t val = (st & 0xE0) | (r8(reg::kOpenBus) & 0x1F);
-                w8(reg::kStatus, st & 0x7F);
-                flags &= ~kNmiPending;
-                w8(reg::kW, 0);
-                w8(reg::kOpenBus, val);
+                const std::uint32_t val = (status() & 0xE0) | (io & 0x1F);
+                io = (io & ~0x80FFu) | val;   // vblank flag cleared, open bus = the value read
+                flags &= ~(kNmiPending | kWToggle);
                 return val;
             }
             if (reg == 4) return vmem()[vram::kOam + r8(reg::kOamAddr)];
@@ -266,28 +287,27 @@ struct Console {
                     w8(reg::kReadBuffer, vram_rd(va));
                 }
                 w16(reg::kV, v + ((r8(reg::kCtrl) & 0x04) ? 32u : 1u));
-                w8(reg::kOpenBus, val);
+                set_open_bus(val);
                 return val;
             }
-            return r8(reg::kOpenBus);
+            return open_bus();
         }
         if (addr == 0x4016) {
-            if (r8(reg::kStrobe)) return 0x40 | (r8(reg::kC1Buttons) & 1);
+            if (flags & kStrobeBit) return 0x40 | (buttons() & 1);
             std::uint32_t bit = 1;
-            const std::uint32_t n = r8(reg::kC1Count);
+            const std::uint32_t n = c1_count();
             if (n < 8) {
-                const std::uint32_t sh = r8(reg::kC1Shift);
+                const std::uint32_t sh = c1_shift();
                 bit = sh & 1;
-                w8(reg::kC1Shift, sh >> 1);
-                w8(reg::kC1Count, n + 1);
+                set_c1(sh >> 1, n + 1);
             }
             return 0x40 | bit;
         }
         if (addr == 0x4017) {
-            if (r8(reg::kStrobe)) return 0x40;
-            const std::uint32_t n = r8(reg::kC2Count);
+            if (flags & kStrobeBit) return 0x40;
+            const std::uint32_t n = c2_count();
             if (n < 8) {
-                w8(reg::kC2Count, n + 1);
+                set_c2_count(n + 1);
                 return 0x40;
             }
             return 0x41;
@@ -297,10 +317,10 @@ struct Console {
     }
 
     __device__ void ppu_wr(std::uint32_t r, std::uint32_t val) {
-        w8(reg::kOpenBus, val);
+        set_open_bus(val);
         if (r == 0) {
             const std::uint32_t ctrl = r8(reg::kCtrl);
-            if ((val & 0x80) && !(ctrl & 0x80) && (r8(reg::kStatus) & 0x80)) flags |= kNmiPending;
+            if ((val & 0x80) && !(ctrl & 0x80) && (status() & 0x80)) flags |= kNmiPending;
             w8(reg::kCtrl, val);
             w16(reg::kT, (r16(reg::kT) & 0xF3FF) | ((val & 0x03) << 10));
         } else if (r == 1) {
@@ -313,27 +333,25 @@ struct Console {
             w8(reg::kOamAddr, oa + 1);
         } else if (r == 5) {
             const std::uint32_t t = r16(reg::kT);
-            if (!r8(reg::kW)) {
+            if (!(flags & kWToggle)) {
                 w8(reg::kFineX, val & 7);
                 w16(reg::kT, (t & 0xFFE0) | (val >> 3));
                 w8(reg::kScrollX, val);
-                w8(reg::kW, 1);
             } else {
                 w16(reg::kT, (((t & 0x8FFF) | ((val & 0x07) << 12)) & 0xFC1F) | ((val & 0xF8) << 2));
                 w8(reg::kScrollY, val);
-                w8(reg::kW, 0);
             }
+            flags ^= kWToggle;
         } else if (r == 6) {
             const std::uint32_t t = r16(reg::kT);
-            if (!r8(reg::kW)) {
+            if (!(flags & kWToggle)) {
                 w16(reg::kT, (t & 0x00FF) | ((val & 0x3F) << 8));
-                w8(reg::kW, 1);
             } else {
                 const std::uint32_t nt = (t & 0x7F00) | val;
                 w16(reg::kT, nt);
                 w16(reg::kV, nt);
-                w8(reg::kW, 0);
             }
+            flags ^= kWToggle;
         } else if (r == 7) {
             const std::uint32_t v = r16(reg::kV);
             vram_wr(v, val);
@@ -356,12 +374,11 @@ struct Console {
         }
         if (addr == 0x4016) {
             const std::uint32_t next = val & 1;
-            if (next || r8(reg::kStrobe)) {
-                w8(reg::kC1Shift, r8(reg::kC1Buttons));
-                w8(reg::kC1Count, 0);
-                w8(reg::kC2Count, 0);
+            if (next || (flags & kStrobeBit)) {
+                set_c1(buttons(), 0);
+                set_c2_count(0);
             }
-            w8(reg::kStrobe, next);
+            flags = next ? (flags | kStrobeBit) : (flags & ~kStrobeBit);
         }
         return 0;
     }
@@ -384,7 +401,7 @@ struct Console {
     __device__ std::uint32_t settle(std::uint32_t dots, bool every_vblank) {
         const std::uint32_t start = r32(reg::kFrameDot), end = start + dots;
         const std::uint32_t fc = end >= kFrameDots ? 1u : 0u;
-        std::uint32_t status = r8(reg::kStatus);
+        std::uint32_t status = this->status();
         const std::uint32_t mask = r8(reg::kMask), ctrl = r8(reg::kCtrl);
         for (std::uint32_t fo = 0; fo <= fc; ++fo) {
             const std::uint32_t off = fo * kFrameDots;
@@ -406,7 +423,7 @@ struct Console {
                 }
             }
         }
-        w8(reg::kStatus, status);
+        set_status(status);
         w32(reg::kFrameDot, end - fc * kFrameDots);
         return fc;
     }
@@ -493,9 +510,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             for (std::uint32_t ra = 0x180; ra < 0x200; ra += 4) stage(ra, C::ram_lds_off(ra));
         }
         // PPU and pad registers, and the loop state kept off the hot path.
-        c.w8(reg::kCtrl, s.ctrl[env]); c.w8(reg::kMask, s.mask[env]); c.w8(reg::kStatus, s.status[env]);
-        c.w8(reg::kOamAddr, s.oam_addr[env]); c.w8(reg::kOpenBus, s.open_bus[env]);
-        c.w8(reg::kReadBuffer, s.read_buffer[env]); c.w8(reg::kFineX, s.fine_x[env]); c.w8(reg::kW, s.w[env]);
+        c.w8(reg::kCtrl, s.ctrl[env]); c.w8(reg::kMask, s.mask[env]);
+        c.w8(reg::kOamAddr, s.oam_addr[env]);
+        c.w8(reg::kReadBuffer, s.read_buffer[env]); c.w8(reg::kFineX, s.fine_x[env]);
         c.w8(reg::kScrollX, s.scroll_x[env]); c.w8(reg::kScrollY, s.scroll_y[env]);
         c.w16(reg::kV, s.v[env]); c.w16(reg::kT, s.t[env]);
         fd0 = s.frame_dot[env];
@@ -504,20 +521,18 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         c.w32(reg::kHorizon, horizon0);
         // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
         const std::uint32_t buttons = s.actions[env], strobe = s.strobe[env];
-        c.w8(reg::kC1Buttons, buttons);
-        c.w8(reg::kC1Shift, strobe ? buttons : s.c1_shift[env]);
-        c.w8(reg::kC1Count, strobe ? 0u : s.c1_count[env]);
-        c.w8(reg::kStrobe, strobe);
-        c.w8(reg::kC2Count, s.c2_count[env]);
+        c.io = s.open_bus[env] | (s.status[env] << 8) | ((strobe ? buttons : s.c1_shift[env]) << 16) |
+               ((strobe ? 0u : s.c1_count[env] & 0xFu) << 24) | (static_cast<std::uint32_t>(s.c2_count[env] & 0xF) << 28);
         c.pc = s.pc[env];
         c.regs = s.a[env] | (s.x[env] << 8) | (s.y[env] << 16) | (static_cast<std::uint32_t>(s.sp[env]) << 24);
         c.p = s.p[env];
-        c.flags = (s.nmi_pending[env] ? kNmiPending : 0u) | (s.fault[env] ? kFault : 0u);
+        c.flags = (s.nmi_pending[env] ? kNmiPending : 0u) | (s.fault[env] ? kFault : 0u) | (s.w[env] ? kWToggle : 0u) |
+                  (strobe ? kStrobeBit : 0u) | (buttons << 8);
         c.w32(reg::kFramesLeft, (c.flags & kFault) ? 0u : frameskip);
         c.w32(reg::kFrames, 0);
         c.w32(reg::kBudgetHits, 0);
     } else {
-        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.flags = 0;
+        c.pc = 0x8000; c.regs = 0; c.p = 0x20; c.flags = 0; c.io = 0;
     }
     __syncthreads();
     c.nmi_vec = lds[0x7FFA] | (lds[0x7FFB] << 8);
@@ -873,23 +888,23 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     s.frame[env] += frames;
     s.frame_dot[env] = fd;
     s.nmi_pending[env] = static_cast<std::uint8_t>((c.flags & kNmiPending) ? 1 : 0);
-    s.status[env] = static_cast<std::uint8_t>(c.r8(reg::kStatus));
+    s.status[env] = static_cast<std::uint8_t>(c.status());
     s.ctrl[env] = static_cast<std::uint8_t>(c.r8(reg::kCtrl));
     s.mask[env] = static_cast<std::uint8_t>(c.r8(reg::kMask));
     s.oam_addr[env] = static_cast<std::uint8_t>(c.r8(reg::kOamAddr));
-    s.open_bus[env] = static_cast<std::uint8_t>(c.r8(reg::kOpenBus));
+    s.open_bus[env] = static_cast<std::uint8_t>(c.open_bus());
     s.read_buffer[env] = static_cast<std::uint8_t>(c.r8(reg::kReadBuffer));
     s.v[env] = static_cast<std::uint16_t>(c.r16(reg::kV));
     s.t[env] = static_cast<std::uint16_t>(c.r16(reg::kT));
     s.fine_x[env] = static_cast<std::uint8_t>(c.r8(reg::kFineX));
-    s.w[env] = static_cast<std::uint8_t>(c.r8(reg::kW));
+    s.w[env] = static_cast<std::uint8_t>((c.flags & kWToggle) ? 1 : 0);
     s.scroll_x[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollX));
     s.scroll_y[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollY));
-    s.c1_buttons[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Buttons));
-    s.c1_shift[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Shift));
-    s.c1_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC1Count));
-    s.strobe[env] = static_cast<std::uint8_t>(c.r8(reg::kStrobe));
-    s.c2_count[env] = static_cast<std::uint8_t>(c.r8(reg::kC2Count));
+    s.c1_buttons[env] = static_cast<std::uint8_t>(c.buttons());
+    s.c1_shift[env] = static_cast<std::uint8_t>(c.c1_shift());
+    s.c1_count[env] = static_cast<std::uint8_t>(c.c1_count());
+    s.strobe[env] = static_cast<std::uint8_t>((c.flags & kStrobeBit) ? 1 : 0);
+    s.c2_count[env] = static_cast<std::uint8_t>(c.c2_count());
     const bool fault = (c.flags & kFault) != 0;
     s.fault[env] = static_cast<std::uint8_t>(fault ? 1 : 0);
 
