@@ -641,10 +641,19 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const std::uint32_t m_lds = rom ? rom_v : ram_v;
         std::uint32_t M = (rd && (rom || ram_lds)) ? m_lds : b1;
         M = sel(d13, w1, M);
-        if (rd && glob) M = s.ram[c.goff(row)];
-        if (rd && io) {
-            M = c.io_rd(ea);
-            vmem_settled();
+        if (kFull) {
+            // All RAM in LDS: I/O reads first (measured faster in this layout).
+            if (rd && io) {
+                M = c.io_rd(ea);
+                vmem_settled();
+            }
+            if (rd && glob) M = s.ram[c.goff(row)];
+        } else {
+            if (rd && glob) M = s.ram[c.goff(row)];
+            if (rd && io) {
+                M = c.io_rd(ea);
+                vmem_settled();
+            }
         }
 
         // Adder, logic unit and right shifter.
