@@ -266,6 +266,7 @@ struct Console {
     // ---- I/O space $2000-$5FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
     //      controller.hpp:20-47) ----------------------------------------------------
     __device__ std::uint32_t io_rd(std::uint32_t addr) {
+        if (addr >= 0x6000) return s.ram[goff(addr - 0x5800)];   // PRG RAM
         if (addr < 0x4000) {
             const std::uint32_t reg = addr & 7;
             if (reg == 2) {
@@ -361,6 +362,10 @@ struct Console {
 
     // Returns the extra PPU dots the write costs (OAM DMA: 513 CPU cycles).
     __device__ std::uint32_t io_wr(std::uint32_t addr, std::uint32_t val) {
+        if (addr >= 0x6000) {   // PRG RAM
+            s.ram[goff(addr - 0x5800)] = static_cast<std::uint8_t>(val);
+            return 0;
+        }
         if (addr < 0x4000) {
             ppu_wr(addr & 7, val);
             return 0;
@@ -557,16 +562,20 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         vmem_settled();
     };
     if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
+    // A pending NMI is taken before the next instruction: its entry stands in
+    // for the fetched opcode (the opcode is fetched again after RTI).
+    if (c.flags & kNmiPending) op = mc::kNmiEntry;
 
     // Every lane runs the whole datapath each iteration.  A lane that has
     // finished its frames runs the NOP entry (changes nothing) and a pending
     // NMI runs as its own entry, so the commit needs no selects; only memory
     // and I/O side paths and the rare control cases branch.
     vmem_settled();  // the state loads above complete before the loop
-    while (__ballot(active) != 0) {
+    // The loop ends when no lane is active; lanes only stop in the rare work,
+    // so only that path tests it.
+    if (__builtin_amdgcn_ballot_w64(active) != 0) for (;;) {
         const std::uint32_t pc0 = c.pc, regs0 = c.regs, p0 = c.p;
-        const bool nmi = (c.flags & kNmiPending) != 0;
-        const std::uint32_t mi = active ? (nmi ? mc::kNmiEntry : op) : mc::kNopEntry;
+        const std::uint32_t mi = active ? op : mc::kNopEntry;
         const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
         const uint4 ma = *reinterpret_cast<const uint4*>(mw);
         const uint4 mb = *reinterpret_cast<const uint4*>(mw + kMicroQuarter);
@@ -634,10 +643,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // PRG RAM), I/O registers, the immediate byte or the pulled byte.
         const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
         const bool ram_lds = is_ram && C::ram_in_lds(ea & 0x7FF);
-        const bool glob = !rom && !ram_lds && (is_ram || ea >= 0x6000);
-        const bool io = !is_ram && ea < 0x6000;
+        // HBM operands: RAM rows outside LDS.  PRG RAM ($6000-$7FFF) goes
+        // with the I/O registers through the side path.
+        const bool glob = is_ram && !ram_lds;
+        const bool io = !is_ram && !rom;
         const bool rd = d0 & 0x100, wr = d0 & 0x200;
-        const std::uint32_t row = is_ram ? (ea & 0x7FF) : ea - 0x5800;
+        const std::uint32_t row = ea & 0x7FF;
         const std::uint32_t m_lds = rom ? rom_v : ram_v;
         std::uint32_t M = (rd && (rom || ram_lds)) ? m_lds : b1;
         M = sel(d13, w1, M);
@@ -713,7 +724,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const bool budget = kBudget && counted && in_frame >= max_instr;
         const bool rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
                           (next - 0x8000u) > 0x7FFDu;
-        if (__ballot(rare) == 0) {
+        if (__builtin_amdgcn_ballot_w64(rare) == 0) {
             left -= static_cast<std::int32_t>(dots);
             continue;
         }
@@ -852,8 +863,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         c.flags &= ~kPresentPending;
         // Code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through the bus,
-        // in order, once the PPU has settled.
+        // in order, once the PPU has settled.  NMI pending (set only here, by
+        // a $2000 write or the vblank event): its entry runs next.
         if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
+        if (c.flags & kNmiPending) op = mc::kNmiEntry;
+        if (__builtin_amdgcn_ballot_w64(active) == 0) break;
     }
 
     if (!mine) return;
