@@ -628,7 +628,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         {
             const std::uint32_t off = next & 0x7FFF;
             op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
-            opaque(op_n); opaque(b1_n); opaque(b2_n);
+            if (!kFull) {   // measured: the barrier helps the split layout only
+                opaque(op_n); opaque(b1_n); opaque(b2_n);
+            }
         }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
