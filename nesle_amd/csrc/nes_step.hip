@@ -73,11 +73,12 @@ constexpr std::uint32_t kLdsRam = kLdsMicro + mc::kEntries * kMicroBytes; // con
 // odd number of dwords, so lanes at equal offsets hit distinct banks.
 constexpr std::uint32_t kSplitStride = 428;     // $0180-$01FF, $0000-$00FF, spare, registers
 constexpr std::uint32_t kFullStride = 2092;     // $0000-$07FF, spare, registers
-// Register area offsets (bytes from the start of the area).
+// Register area offsets (bytes from the start of the area).  Bytes 2, 4, 7
+// and 10-14 are unused: PPUSTATUS, open bus, the write toggle and the pad
+// registers stay in VGPRs for the whole launch.
 namespace reg {
-constexpr std::uint32_t kCtrl = 0, kMask = 1, kStatus = 2, kOamAddr = 3, kOpenBus = 4, kReadBuffer = 5;
-constexpr std::uint32_t kFineX = 6, kW = 7, kScrollX = 8, kScrollY = 9, kC1Buttons = 10, kC1Shift = 11;
-constexpr std::uint32_t kC1Count = 12, kStrobe = 13, kC2Count = 14, kDmaPage = 15, kV = 16, kT = 18;
+constexpr std::uint32_t kCtrl = 0, kMask = 1, kOamAddr = 3, kReadBuffer = 5;
+constexpr std::uint32_t kFineX = 6, kScrollX = 8, kScrollY = 9, kDmaPage = 15, kV = 16, kT = 18;
 constexpr std::uint32_t kFrameDot = 20, kHorizon = 24, kFramesLeft = 28, kFrames = 32, kBudgetHits = 36;
 constexpr std::uint32_t kBytes = 40;
 }  // namespace reg
