@@ -30,7 +30,8 @@
 //    status, open bus, write toggle, pads) are packed into VGPRs, so those
 //    reads take no LDS round trip; the other PPU registers live in a
 //    per-console LDS area.
-//  * Only the HBM operand and the I/O register read branch inside the loop;
+//  * Only the HBM operand load and the I/O register read branch inside the
+//    loop (PPUSTATUS and pad 1 reads by selects, the rest behind a branch);
 //    everything rare (I/O writes, JMP indirect, stack wrap, idle loops,
 //    illegal opcodes, PPU events, OAM DMA, code outside ROM) sits behind one
 //    wave-uniform test.
@@ -80,7 +81,6 @@ namespace reg {
 constexpr std::uint32_t kCtrl = 0, kMask = 1, kOamAddr = 3, kReadBuffer = 5;
 constexpr std::uint32_t kFineX = 6, kScrollX = 8, kScrollY = 9, kDmaPage = 15, kV = 16, kT = 18;
 constexpr std::uint32_t kFrameDot = 20, kHorizon = 24, kFramesLeft = 28, kFrames = 32, kBudgetHits = 36;
-constexpr std::uint32_t kBytes = 40;
 }  // namespace reg
 
 // Bits of a console's `flags` VGPR.
@@ -92,7 +92,8 @@ constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4, kPresentPe
 constexpr std::uint32_t kWToggle = 16, kStrobeBit = 32;
 
 // Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
-// write to (one spare byte per console after PRG RAM).
+// write to (one spare byte per console after PRG RAM; lanes without a console
+// use console 0's), so the operand store needs no branch.
 constexpr std::uint32_t kTrashRow = kRamBytes + kPrgRamBytes;
 
 // Lanes without a console run the datapath on a dummy block after the last
@@ -262,6 +263,27 @@ struct Console {
             return;
         }
         vmem()[vram::kPalette + pal_index(addr)] = static_cast<std::uint8_t>(val);
+    }
+
+    // An I/O read: PPUSTATUS (and mirrors) and pad 1, the common ones, by
+    // selects for every lane of the side path; the others through io_rd.
+    __device__ std::uint32_t io_read(std::uint32_t addr) {
+        const bool r2002 = (addr & 0xE007) == 0x2002;
+        const bool r4016 = addr == 0x4016;
+        const std::uint32_t v2002 = (status() & 0xE0) | (io & 0x1F);
+        const bool strobe = (flags & kStrobeBit) != 0;
+        const std::uint32_t n = c1_count(), sh = c1_shift();
+        const bool shifting = r4016 && !strobe && n < 8;
+        const std::uint32_t bit = strobe ? (buttons() & 1) : (n < 8 ? (sh & 1) : 1u);
+        std::uint32_t io_n = r2002 ? ((io & ~0x80FFu) | v2002) : io;
+        io = shifting ? ((io_n & 0xF000FFFFu) | ((sh >> 1) << 16) | ((n + 1) << 24)) : io_n;
+        flags = r2002 ? (flags & ~(kNmiPending | kWToggle)) : flags;
+        std::uint32_t v = r2002 ? v2002 : (0x40 | bit);
+        if (!r2002 && !r4016) {
+            v = io_rd(addr);
+            vmem_settled();
+        }
+        return v;
     }
 
     // ---- I/O space $2000-$5FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
@@ -572,28 +594,67 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     // NMI runs as its own entry, so the commit needs no selects; only memory
     // and I/O side paths and the rare control cases branch.
     vmem_settled();  // the state loads above complete before the loop
+
+    // Decode of the instruction about to run: microcode slices 0 and 4
+    // (addressing, operand and ALU control), effective address, page-cross
+    // flag and, in the split layout, the HBM operand.  The split layout
+    // decodes one iteration ahead: at the end of an iteration (after its
+    // memory writes, on which the decode may depend) or after rare work, so
+    // the HBM operand load has a whole iteration to arrive and the operand
+    // LDS reads go out with the microcode reads.  With all RAM in LDS (no HBM
+    // operand) the decode at the top of the iteration measured faster.
+    uint4 ma_c, me_c;
+    std::uint32_t ea_c = 0, cross_c = 0, gval_c = 0;
+    auto slices = [&](std::uint32_t mi) {
+        const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
+        ma_c = *reinterpret_cast<const uint4*>(mw);
+        me_c = *reinterpret_cast<const uint4*>(mw + 4 * kMicroQuarter);
+    };
+    // Zero-page pointer of (zp,X) / (zp),Y (opcode bits select X).
+    auto zp_pointer = [&](std::uint32_t o, std::uint32_t lo, std::uint32_t regs) {
+        const std::uint32_t pz = (lo + (((o & 0x1F) == 0x01) ? ubfe(regs, 8, 8) : 0u)) & 0xFF;
+        return lds[base + C::kZp + pz] | (lds[base + C::kZp + ((pz + 1) & 0xFF)] << 8);
+    };
+    auto address_at = [&](std::uint32_t ptr, std::uint32_t lo, std::uint32_t hi, std::uint32_t regs) {
+        const std::uint32_t abs = lo | (hi << 8);
+        const std::uint32_t ebase = sel(me_c.x, ptr, abs);
+        const std::uint32_t ea_full = ebase + ubfe(regs, ma_c.x, ma_c.y);
+        ea_c = ea_full & me_c.y;
+        cross_c = ((ea_full ^ ebase) >> 8) & (ma_c.x >> 7) & 1;
+        if constexpr (!kFull) {
+            // Every lane loads (no branch); lanes without an HBM operand read
+            // row 0, one cache line for the wave, and ignore the byte.
+            const bool g = (ma_c.x & 0x100) && ea_c < 0x2000 && !C::ram_in_lds(ea_c & 0x7FF);
+            gval_c = s.ram[c.goff(g ? (ea_c & 0x7FF) : 0u)];
+        }
+    };
+    auto address = [&](std::uint32_t o, std::uint32_t lo, std::uint32_t hi, std::uint32_t regs) {
+        address_at(zp_pointer(o, lo, regs), lo, hi, regs);
+    };
+    if constexpr (!kFull) {
+        slices(active ? op : mc::kNopEntry);
+        address(op, b1, b2, c.regs);
+    }
     // The loop ends when no lane is active; lanes only stop in the rare work,
     // so only that path tests it.
     if (__builtin_amdgcn_ballot_w64(active) != 0) for (;;) {
         const std::uint32_t pc0 = c.pc, regs0 = c.regs, p0 = c.p;
         const std::uint32_t mi = active ? op : mc::kNopEntry;
         const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
-        const uint4 ma = *reinterpret_cast<const uint4*>(mw);
+        if constexpr (kFull) {
+            slices(mi);
+            address(op, b1, b2, regs0);
+        }
+        const uint4 ma = ma_c, me = me_c;
         const uint4 mb = *reinterpret_cast<const uint4*>(mw + kMicroQuarter);
         const uint4 mcw = *reinterpret_cast<const uint4*>(mw + 2 * kMicroQuarter);
         const uint4 md = *reinterpret_cast<const uint4*>(mw + 3 * kMicroQuarter);
-        const uint4 me = *reinterpret_cast<const uint4*>(mw + 4 * kMicroQuarter);
         const std::uint32_t d0 = ma.x, d1 = ma.y, d2 = ma.z, d3 = ma.w;
         const std::uint32_t d4 = mb.x, d5 = mb.y, d6 = mb.z, d7 = mb.w;
         const std::uint32_t d8 = mcw.x, d9 = mcw.y, d10 = mcw.z, d11 = mcw.w;
         const std::uint32_t d12 = md.x, d13 = md.y, d14 = md.z, d15 = md.w;
-        const std::uint32_t d16 = me.x, d17 = me.y, d18 = me.z, d19 = me.w;
+        const std::uint32_t d16 = me.x, d18 = me.z, d19 = me.w;   // d17: the address mask, used by the decode
 
-        // Zero-page pointer of (zp,X) / (zp),Y (opcode bits select X), read
-        // together with the microcode and the stack window.
-        const std::uint32_t xreg = ubfe(regs0, 8, 8);
-        const std::uint32_t pz = (b1 + (((op & 0x1F) == 0x01) ? xreg : 0u)) & 0xFF;
-        const std::uint32_t ptr = lds[base + C::kZp + pz] | (lds[base + C::kZp + ((pz + 1) & 0xFF)] << 8);
         // Stack window $0100+SP-2 .. $0100+SP+3 (split mode: only when it lies
         // in the LDS half of the page, else a harmless spare area).
         const std::uint32_t sp = regs0 >> 24;
@@ -604,14 +665,21 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
 
         // Effective address and the operand candidates in LDS.
         const std::uint32_t abs = b1 | (b2 << 8);
-        const std::uint32_t ebase = sel(d16, ptr, abs);
-        const std::uint32_t idx = ubfe(regs0, d0, d1);
-        const std::uint32_t ea_full = ebase + idx;
-        const std::uint32_t ea = ea_full & d17;
-        const std::uint32_t cross = ((ea_full ^ ebase) >> 8) & (d0 >> 7) & 1;
+        const std::uint32_t ea = ea_c, cross = cross_c;
         const std::uint32_t rom_v = lds[ea & 0x7FFF];
         const std::uint32_t ram_a = base + C::ram_lds_off(ea);
         const std::uint32_t ram_v = lds[ram_a];
+        // Operand classes.  HBM operands (split layout: RAM rows outside LDS)
+        // were loaded by the decode and are merged after the I/O side path.
+        // PRG RAM ($6000-$7FFF) goes with the I/O registers through the side
+        // path.
+        const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
+        const bool ram_lds = is_ram && C::ram_in_lds(ea & 0x7FF);
+        const bool glob = is_ram && !ram_lds;
+        const bool io = !is_ram && !rom;
+        const bool rd = d0 & 0x100, wr = d0 & 0x200;
+        const std::uint32_t row = ea & 0x7FF;
+        const std::uint32_t gval = gval_c;
 
         // Next PC: fall through, branch, absolute (JMP/JSR), pulled return
         // address (RTS/RTI) or vector (BRK/NMI); its bytes are fetched now.
@@ -633,6 +701,14 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
                 opaque(op_n); opaque(b1_n); opaque(b2_n);
             }
         }
+        // Split layout: slices 0 and 4 of the next instruction's microcode,
+        // for its decode at the end of this iteration.
+        uint4 ma_n = ma, me_n = me;
+        if constexpr (!kFull) {
+            const std::uint8_t* mw_n = lds + kLdsMicro + 16 * (active ? op_n : mc::kNopEntry);
+            ma_n = *reinterpret_cast<const uint4*>(mw_n);
+            me_n = *reinterpret_cast<const uint4*>(mw_n + 4 * kMicroQuarter);
+        }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
         // window contents.
@@ -644,30 +720,19 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
 
         // Operand: LDS (zero page, stack top, PRG ROM), HBM (other RAM rows,
         // PRG RAM), I/O registers, the immediate byte or the pulled byte.
-        const bool is_ram = ea < 0x2000, rom = ea >= 0x8000;
-        const bool ram_lds = is_ram && C::ram_in_lds(ea & 0x7FF);
-        // HBM operands: RAM rows outside LDS.  PRG RAM ($6000-$7FFF) goes
-        // with the I/O registers through the side path.
-        const bool glob = is_ram && !ram_lds;
-        const bool io = !is_ram && !rom;
-        const bool rd = d0 & 0x100, wr = d0 & 0x200;
-        const std::uint32_t row = ea & 0x7FF;
         const std::uint32_t m_lds = rom ? rom_v : ram_v;
         std::uint32_t M = (rd && (rom || ram_lds)) ? m_lds : b1;
         M = sel(d13, w1, M);
         if (kFull) {
-            // All RAM in LDS: I/O reads first (measured faster in this layout).
-            if (rd && io) {
-                M = c.io_rd(ea);
-                vmem_settled();
-            }
-            if (rd && glob) M = s.ram[c.goff(row)];
+            if (rd && io) M = c.io_read(ea);   // all RAM is in LDS: no HBM operand
         } else {
-            if (rd && glob) M = s.ram[c.goff(row)];
-            if (rd && io) {
-                M = c.io_rd(ea);
-                vmem_settled();
-            }
+            // The side path's result has a register of its own: were it
+            // written into M, which shares the HBM load's register, the
+            // compiler would wait for that load before the side path.
+            std::uint32_t mio = 0;
+            if (rd && io) mio = c.io_read(ea);
+            M = (rd && io) ? mio : M;
+            M = (rd && glob) ? gval : M;
         }
 
         // Adder, logic unit and right shifter.
@@ -698,6 +763,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         lds[wb + 2] = static_cast<std::uint8_t>(win >> 16);
         const std::uint32_t waddr = (wr && ram_lds) ? ram_a : spare;
         lds[waddr] = static_cast<std::uint8_t>(r);
+        // Split layout: the next instruction's zero-page pointer, read right
+        // after this instruction's LDS writes (its latency overlaps the
+        // commit and the rare-work test).
+        std::uint32_t ptr_n = 0;
+        if constexpr (!kFull) ptr_n = zp_pointer(op_n, b1_n, regs_n);
 
         // Commit.  The NOP entry leaves everything as it was.
         c.pc = next;
@@ -715,7 +785,6 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
                 atomicAdd(&s.prof_pcs[pc0], 1ull);
             }
         }
-        if (wr && glob) s.ram[c.goff(row)] = static_cast<std::uint8_t>(r);
         // Rare work, tested once per iteration: I/O register writes, JMP
         // ($xxxx), stack bytes outside the LDS window, the idle loop, illegal
         // opcodes, PPU timing events, the frame budget, OAM DMA and code
@@ -727,6 +796,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const bool budget = kBudget && counted && in_frame >= max_instr;
         const bool rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
                           (next - 0x8000u) > 0x7FFDu;
+        if constexpr (!kFull) s.ram[c.goff((wr && glob) ? row : kTrashRow)] = static_cast<std::uint8_t>(r);
+        if constexpr (!kFull) {   // decode of the next instruction
+            ma_c = ma_n; me_c = me_n;
+            address_at(ptr_n, b1_n, b2_n, regs_n);
+        }
         if (__builtin_amdgcn_ballot_w64(rare) == 0) {
             left -= static_cast<std::int32_t>(dots);
             continue;
@@ -871,6 +945,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
         if (c.flags & kNmiPending) op = mc::kNmiEntry;
         if (__builtin_amdgcn_ballot_w64(active) == 0) break;
+        if constexpr (!kFull) {
+            // The rare work may have changed the next instruction, the
+            // registers or RAM: decode again.
+            slices(active ? op : mc::kNopEntry);
+            address(op, b1, b2, c.regs);
+        }
     }
 
     if (!mine) return;
