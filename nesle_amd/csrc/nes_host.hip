@@ -576,7 +576,8 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
         if (stats_mode != 0) {
             b->ensure_stats();
             if (stats_mode == 2) {
-                hip_check(hipMemsetAsync(b->ds.prof_opcodes, 0, 8 * (256 + 65536), b->stream), "clear profile");
+                // Opcode and PC histograms are contiguous.
+                hip_check(nesle::launch_zero_u64(b->ds.prof_opcodes, 256 + 65536, b->stream), "clear profile");
             }
         }
         DeviceState s = b->ds;

@@ -190,6 +190,13 @@ __global__ void __launch_bounds__(kBlock) poke_ram_envs_kernel(DeviceState s, st
     if (env < s.n) s.ram[static_cast<std::size_t>(addr & 0x7FF) * s.pitch + env] = values[env];
 }
 
+// Zero fill of n 64-bit words: a kernel rather than hipMemsetAsync, so that a
+// step that clears its profile histograms can be captured in a HIP graph.
+__global__ void __launch_bounds__(kBlock) zero_u64_kernel(unsigned long long* p, std::uint32_t n) {
+    const std::uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) p[i] = 0ull;
+}
+
 __global__ void __launch_bounds__(kBlock) seed_kernel(DeviceState s) {
     const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
     if (env < s.n) reward_seed(s, env, GlobalRam{s, env});
@@ -270,6 +277,12 @@ hipError_t launch_poke_ram_envs(const DeviceState& s, std::uint32_t addr, const 
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream) {
     if (s.n == 0 || s.present == nullptr) return hipSuccess;
     seed_present_kernel<<<dim3(s.n), dim3(kBlock), 0, stream>>>(s, mask);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_u64(unsigned long long* p, std::uint32_t n, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    zero_u64_kernel<<<dim3(blocks_for(n)), dim3(kBlock), 0, stream>>>(p, n);
     return hipGetLastError();
 }
 

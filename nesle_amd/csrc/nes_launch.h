@@ -15,8 +15,8 @@ namespace nesle {
 hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr,
                        bool auto_reset, int stats_mode, hipStream_t stream);
 // Masked (null = all) reset from the snapshot bank, or power-on without one.
-// The fused auto-reset of a step is this launch with the step's done flags
-// as the mask.
+// The auto-reset after a step is this launch with the step's done flags as
+// the mask.
 hipError_t launch_reset(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
 hipError_t launch_load_blob(const DeviceState& s, const std::uint8_t* blob_src, const std::uint8_t* mask,
                             hipStream_t stream);
@@ -28,6 +28,8 @@ hipError_t launch_poke_ram(const DeviceState& s, std::uint32_t addr, std::uint32
 hipError_t launch_poke_ram_envs(const DeviceState& s, std::uint32_t addr, const std::uint8_t* values,
                                 hipStream_t stream);
 hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
+// n 64-bit words set to zero by a kernel (graph-capturable, unlike a memset).
+hipError_t launch_zero_u64(unsigned long long* p, std::uint32_t n, hipStream_t stream);
 // Presentation snapshot (and pre-render latch) from live state, masked.
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
 

@@ -252,6 +252,49 @@ def test_profile_counts_match_instructions():
     assert set(np.nonzero(ops)[0].tolist()) <= synthrom.OFFICIAL_OPCODES
 
 
+def test_profile_step_clears_and_replays_in_a_graph():
+    """A profiled step clears the opcode/PC histograms with a kernel (no
+    memset), so they count only that step's instructions, eagerly and when
+    the step is captured in a HIP graph: four replays, with eager work and
+    host synchronisations between them, each equal to an eager twin batch
+    (histograms, per-console instruction counts, canonical state)."""
+    import torch
+
+    rom = _rom(4)
+    n = 128
+    say(f"[gpu] profile step in a graph: N={n}")
+    eager = abi.Batch(rom, n, frameskip=4)
+    cap = abi.Batch(rom, n, frameskip=4)
+    stream = torch.cuda.Stream()
+    cap.set_stream(stream.cuda_stream)
+    for b in (eager, cap):
+        b.set_actions(masks_for(6, n, 0))
+        b.step(stats_mode=2)   # first profiled step allocates the statistics
+        b.synchronize()
+    eager.set_actions(masks_for(6, n, 1))
+    eager.step(stats_mode=2)
+    ops, ins = eager.host(abi.VIEW_OPCODES), eager.host(abi.VIEW_INSTRUCTIONS)
+    assert ops.sum() == ins.sum() == eager.host(abi.VIEW_PCS).sum()
+    eager.set_actions(masks_for(6, n, 2))
+    cap.set_actions(masks_for(6, n, 1))
+    cap.step(stats_mode=2)
+    cap.set_actions(masks_for(6, n, 2))
+    cap.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cap.step(stats_mode=2)
+    for k in range(4):
+        graph.replay()
+        eager.step(stats_mode=2)
+        torch.cuda.synchronize()
+        cap.synchronize()
+        for kind in (abi.VIEW_OPCODES, abi.VIEW_PCS, abi.VIEW_INSTRUCTIONS):
+            np.testing.assert_array_equal(cap.host(kind), eager.host(kind), err_msg=f"replay {k} view {kind}")
+        assert cap.host(abi.VIEW_OPCODES).sum() == cap.host(abi.VIEW_INSTRUCTIONS).sum()
+        for e in (0, 63, n - 1):
+            assert np.array_equal(cap.save_state(e), eager.save_state(e)), f"replay {k} env {e}"
+
+
 @pytest.mark.parametrize("num_envs", [64, 16384])
 def test_nrom128_cold_boot_nmi_loop_and_autoreset(num_envs):
     """A 16 KB PRG image (NROM-128) mirrored at $8000 and $C000 (the
