@@ -198,6 +198,55 @@ def test_benchmark_configuration_full_size_sampled():
     assert ends >= len(sample)
 
 
+def test_benchmark_workload_long_run_full_size_sampled():
+    """The benchmark workload over a longer run: 65,536 consoles on the
+    benchmark ROM (seed 2026), 8 snapshot levels, a staggered done countdown
+    poked into every console (episodes end throughout the run, as in the
+    timed window of the benchmark), x-delta reward and auto-reset, 40 steps.
+    64 sampled consoles (wave, workgroup and XCD-range edges, random ones)
+    have the oracle's rewards and dones at every step and its state every
+    eighth step; many episodes end and restart from snapshots meanwhile."""
+    rom = synthrom.make_rom(2026).rom
+    snaps = warm_snapshots(rom, [141, 270, 334, 486, 544, 650, 657, 706], seed=78)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 2 + 2 * i   # episodes of 16-128 frames from a snapshot
+    blobs = [bytes(s) for s in snaps]
+    n, steps = 65536, 40
+    rng = np.random.default_rng(79)
+    levels = rng.integers(0, 8, n).astype(np.uint8)
+    done_init = rng.integers(1, 13, n).astype(np.uint8)   # first episode ends within 24 steps
+    edges = {0, 1, 63, 64, 255, 256, 1023, 1024, 8191, 8192, 16383, 16384, 32767, 32768, 65279, 65280, n - 1}
+    sample = sorted(edges | set(rng.integers(0, n, 64 - len(edges)).tolist()))
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.01)
+    say(f"[gpu] benchmark workload long run: N={n} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.01)
+    b.set_snapshots(blobs, levels)
+    b.poke_ram_envs(synthrom.DONE_BYTE, done_init)
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        c.load(snaps[levels[e]])
+        c.write(synthrom.DONE_BYTE, int(done_init[e]))
+    ends = 0
+    for k in range(steps):
+        m = masks_for(7070, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES)[sample], don, err_msg=f"step {k} dones")
+        for j in np.nonzero(don)[0]:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += int(don.sum())
+        if k % 8 == 7:
+            say(f"[gpu]   step {k}: {ends} sampled episode ends so far")
+            for e, ref in zip(sample, ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert ends >= len(sample) + 16
+
+
 def test_reset_envs_and_state_roundtrip():
     """Masked reset returns exactly the selected consoles to power-on; a saved
     state loaded into other consoles makes them identical; int64 device
