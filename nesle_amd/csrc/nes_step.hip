@@ -84,7 +84,10 @@ constexpr std::uint32_t kFrameDot = 20, kHorizon = 24, kFramesLeft = 28, kFrames
 }  // namespace reg
 
 // Bits of a console's `flags` VGPR.
-constexpr std::uint32_t kNmiPending = 1, kDmaPending = 2, kFault = 4, kPresentPending = 8;
+constexpr std::uint32_t kDmaPending = 1, kNmiPending = 2, kFault = 4, kPresentPending = 8;
+// The microcode's clear-NMI bit is the flag's own bit, so the commit clears it
+// with one and-not.
+static_assert(kNmiPending == mc::kClearNmi, "NMI flag and clear bit must match");
 // The PPU and pad registers every I/O read touches live in VGPRs: the write
 // toggle and pad strobe as `flags` bits, pad 1's buttons in `flags` bits
 // 8-15, and `io` = open bus (bits 0-7) | PPUSTATUS (8-15) | pad 1 shift
@@ -799,7 +802,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         c.pc = next;
         c.regs = regs_n;
         c.p = pn;
-        c.flags &= ~((d14 >> 1) & kNmiPending);
+        c.flags &= ~(d14 & mc::kClearNmi);
         op = op_n; b1 = b1_n; b2 = b2_n;
         std::uint32_t dots = 3 * ((d16 >> 16) + cross + (taken ? bcyc : 0u));
         const std::uint32_t counted = d14 & mc::kCount;
