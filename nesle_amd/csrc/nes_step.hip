@@ -127,10 +127,6 @@ __device__ __forceinline__ std::uint32_t sel(std::uint32_t m, std::uint32_t a, s
     return (a & m) | (b & ~m);
 }
 
-// Instruction bytes are carried across iterations as 32-bit values already
-// zero-extended by the LDS byte read; hiding them from the optimizer keeps it
-// from narrowing the loop-carried value to 8 bits and re-extending it.
-__device__ __forceinline__ void opaque(std::uint32_t& v) { asm("" : "+v"(v)); }
 
 __device__ __forceinline__ std::uint32_t ubfe(std::uint32_t v, std::uint32_t off, std::uint32_t w) {
     return __builtin_amdgcn_ubfe(v, off, w);
@@ -720,17 +716,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             } else {
                 op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
             }
-            if (!kFull) {   // measured: the barrier helps the split layout only
-                opaque(op_n); opaque(b1_n); opaque(b2_n);
-            }
-        }
-        // Split layout: slices 0 and 4 of the next instruction's microcode,
-        // for its decode at the end of this iteration.
-        uint4 ma_n = ma, me_n = me;
-        if constexpr (!kFull) {
-            const std::uint8_t* mw_n = lds + kLdsMicro + 16 * (active ? op_n : mc::kNopEntry);
-            ma_n = *reinterpret_cast<const uint4*>(mw_n);
-            me_n = *reinterpret_cast<const uint4*>(mw_n + 4 * kMicroQuarter);
+
         }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
@@ -796,7 +782,15 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // after this instruction's LDS writes (its latency overlaps the
         // commit and the rare-work test).
         std::uint32_t ptr_n = 0;
-        if constexpr (!kFull) ptr_n = zp_pointer(op_n, b1_n, regs_n);
+        uint4 ma_n = ma, me_n = me;
+        if constexpr (!kFull) {
+            ptr_n = zp_pointer(op_n, b1_n, regs_n);
+            // Slices 0 and 4 of the next instruction's microcode, read
+            // together with its pointer.
+            const std::uint8_t* mw_n = lds + kLdsMicro + 16 * (active ? op_n : mc::kNopEntry);
+            ma_n = *reinterpret_cast<const uint4*>(mw_n);
+            me_n = *reinterpret_cast<const uint4*>(mw_n + 4 * kMicroQuarter);
+        }
 
         // Commit.  The NOP entry leaves everything as it was.
         c.pc = next;
