@@ -716,7 +716,6 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             } else {
                 op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
             }
-
         }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
