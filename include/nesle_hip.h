@@ -107,10 +107,14 @@ typedef struct nesle_rom_info {
 /* Defaults: SMB reward, frameskip 4, budget 200,000, current device, frames on. */
 void nesle_config_init(nesle_config* cfg);
 
+/* Largest batch: the step kernel addresses the interleaved RAM/PRG-RAM rows
+ * (10,241 rows of round_up(num_envs, 256) bytes) with 32-bit offsets. */
+#define NESLE_MAX_ENVS 262144u
+
 /* Parse the iNES image, allocate device state, upload PRG/CHR and power every
  * console on.  Replaces CudaBatchBinding(num_envs, frameskip, rom_bytes):
  * cuda_module.cu:389-411 (+ allocate 978-1118, upload_rom 1209-1225,
- * reset_console 1227-1289). */
+ * reset_console 1227-1289).  num_envs must be 1..NESLE_MAX_ENVS. */
 int nesle_create(const nesle_config* cfg, const uint8_t* ines, size_t ines_len, nesle_batch** out);
 
 /* Install a snapshot bank (FCEUX FCS or canonical NST1 blobs, detected by

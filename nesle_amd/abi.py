@@ -29,6 +29,7 @@ VIEW_FRAME_RGB, VIEW_FRAME_PALETTE, VIEW_GRAY84 = 10, 11, 12
 FRAME_RGB, FRAME_PALETTE, FRAME_GRAY84 = 1, 2, 4
 DTYPE_U8, DTYPE_I64, DTYPE_F32, DTYPE_U32, DTYPE_U64 = 0, 1, 2, 3, 4
 STATE_BYTES = 22896
+MAX_ENVS = 262144   # NESLE_MAX_ENVS
 
 _U8P = ctypes.POINTER(ctypes.c_uint8)
 

@@ -431,6 +431,8 @@ int nesle_create(const nesle_config* cfg, const std::uint8_t* ines, std::size_t 
         if (out == nullptr || cfg == nullptr) throw InvalidArgument("null argument");
         *out = nullptr;
         if (cfg->num_envs == 0) throw InvalidArgument("num_envs must be positive");
+        if (cfg->num_envs > NESLE_MAX_ENVS)
+            throw InvalidArgument("num_envs must be at most " + std::to_string(NESLE_MAX_ENVS));
         if (cfg->frameskip == 0) throw InvalidArgument("frameskip must be positive");
         if (cfg->reward_kind > NESLE_REWARD_XDELTA) throw InvalidArgument("unknown reward_kind");
         auto b = std::make_unique<nesle_batch>();

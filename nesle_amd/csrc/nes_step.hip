@@ -1057,8 +1057,12 @@ struct Geometry {
 // smallest power-of-two L with 256 CUs x W x L >= n.  W trades issue slots for
 // latency hiding: W/4 waves share each SIMD.
 Geometry geometry(std::uint32_t n, std::uint32_t waves) {
+    // More consoles per wave while the batch needs them and the workgroup's
+    // consoles still fit in LDS with at least the split layout.
     std::uint32_t lane_bits = 0;
-    while (lane_bits < 6 && ((256u * waves) << lane_bits) < n) ++lane_bits;
+    while (lane_bits < 6 && ((256u * waves) << lane_bits) < n &&
+           lds_bytes(waves << (lane_bits + 1), false) <= kLdsLimit)
+        ++lane_bits;
     Geometry g{};
     g.waves = waves;
     g.lane_bits = lane_bits;
@@ -1100,6 +1104,7 @@ hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint3
                        int stats_mode, hipStream_t stream) {
     Geometry g = geometry(s.n, waves_per_group());
     if (g.full && g.waves != 4) g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
+    if (g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
     // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
     const bool budget = max_instr < 15000;
     hipError_t e;

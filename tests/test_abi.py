@@ -28,6 +28,11 @@ def test_library_exports_every_declared_function():
     assert not missing, f"declared but not exported: {missing}"
 
 
+def test_binding_constants_match_the_header():
+    text = abi.HEADER.read_text()
+    assert f"#define NESLE_MAX_ENVS {abi.MAX_ENVS}u" in text
+
+
 def test_parse_ines_known_answers():
     """tests/cpp/test_core.cpp:33-100."""
     info = abi.parse_ines(_ines())
@@ -70,6 +75,7 @@ def test_create_rejects_bad_arguments_before_touching_a_device():
     rom = synthrom.make_rom(1).rom
     L = abi.lib()
     assert _create(0, 4, rom) == abi.EINVAL and "num_envs" in L.nesle_last_error().decode()
+    assert _create(abi.MAX_ENVS + 1, 4, rom) == abi.EINVAL and "at most" in L.nesle_last_error().decode()
     assert _create(8, 0, rom) == abi.EINVAL and "frameskip" in L.nesle_last_error().decode()
     assert _create(8, 4, rom, reward_kind=7) == abi.EINVAL
     assert _create(8, 4, b"NES") == abi.EINVAL

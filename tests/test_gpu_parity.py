@@ -198,6 +198,32 @@ def test_benchmark_configuration_full_size_sampled():
     assert ends >= len(sample)
 
 
+def test_largest_batch_sampled():
+    """The largest batch, NESLE_MAX_ENVS = 262,144 consoles: 1,024 workgroups
+    of 256 consoles, four to a compute unit in turn, and RAM/PRG-RAM offsets up
+    to 2.7e9.  Sampled consoles at workgroup-round and range edges equal the
+    oracle (instruction counts and rewards every step, state at the end)."""
+    rom = _rom(2026)
+    n = abi.MAX_ENVS
+    rng = np.random.default_rng(11)
+    sample = sorted({0, 255, 256, 65535, 65536, 131071, 131072, 196607, 196608, n - 257, n - 256, n - 1,
+                     *rng.integers(0, n, 8).tolist()})
+    say(f"[gpu] largest batch: N={n} fs=4 sample={sample}")
+    b = abi.Batch(rom, n, frameskip=4)
+    ob = OracleBatch(rom, sample)
+    for k in range(4):
+        m = masks_for(99, n, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, _ = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS)[sample], ins, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k}")
+    for e, ref in zip(sample, ob.states()):
+        got = b.save_state(e)
+        assert np.array_equal(got, ref), f"env {e}: {first_diff(got, ref)}"
+    b.close()
+
+
 def test_benchmark_workload_long_run_full_size_sampled():
     """The benchmark workload over a longer run: 65,536 consoles on the
     benchmark ROM (seed 2026), 8 snapshot levels, a staggered done countdown
