@@ -311,6 +311,52 @@ def test_reset_envs_and_state_roundtrip():
     np.testing.assert_array_equal(b2.host(abi.VIEW_RAM), b3.host(abi.VIEW_RAM))
 
 
+def test_full_size_snapshot_reset_properties():
+    """Size-independent properties at 65,536 consoles with 8 snapshot levels:
+    two batches fed the same actions stay identical (RAM of every console);
+    a snapshot captured from a console exports its state byte for byte; a
+    masked reset puts every masked console's RAM (and, sampled, its whole
+    state) exactly into its level's snapshot and leaves every other console's
+    RAM untouched; the same reset again changes nothing."""
+    rom = synthrom.make_rom(2026).rom
+    snaps = warm_snapshots(rom, [120, 240, 360, 480, 600, 720, 840, 960], seed=21)
+    blobs = [bytes(x) for x in snaps]
+    n = 65536
+    rng = np.random.default_rng(21)
+    levels = rng.integers(0, 8, n).astype(np.uint8)
+    say(f"[gpu] full-size snapshot/reset properties: N={n}")
+    a = abi.Batch(rom, n, frameskip=4)
+    b = abi.Batch(rom, n, frameskip=4)
+    for x in (a, b):
+        x.set_snapshots(blobs, levels)
+    for k in range(6):
+        m = masks_for(21, n, k)
+        for x in (a, b):
+            x.set_actions(m)
+            x.step()
+    before = a.host(abi.VIEW_RAM)
+    np.testing.assert_array_equal(before, b.host(abi.VIEW_RAM))
+    b.close()
+    for e, slot in ((12345, 3), (n - 1, 5)):
+        st = a.save_state(e)
+        a.snapshot_capture(e, slot)
+        assert np.array_equal(a.snapshot_export(slot), st), f"capture of env {e}"
+    bank = [a.snapshot_export(lv) for lv in range(8)]
+    mask = (rng.random(n) < 1 / 7).astype(np.uint8)
+    a.reset_envs(mask)
+    after = a.host(abi.VIEW_RAM)
+    keep = mask == 0
+    np.testing.assert_array_equal(after[keep], before[keep])
+    ram = O.OFF["ram"]
+    expect = np.stack([bk[ram:ram + 2048] for bk in bank])
+    np.testing.assert_array_equal(after[~keep], expect[levels[~keep]])
+    masked = np.nonzero(mask)[0]
+    for e in masked[:: max(1, len(masked) // 16)][:16]:
+        assert np.array_equal(a.save_state(int(e)), bank[levels[e]]), f"reset env {e}"
+    a.reset_envs(mask)
+    np.testing.assert_array_equal(a.host(abi.VIEW_RAM), after)
+
+
 def test_profile_counts_match_instructions():
     """step_profile's opcode histogram sums to the per-console instruction
     counts; only official opcodes appear."""
