@@ -659,19 +659,13 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const std::uint32_t sp = regs0 >> 24;
         std::uint32_t wb = base + C::kStk + sp;
         if (!kFull) wb = sp >= 0x82u ? wb : spare;
-        std::uint32_t o2, o1, o0, w1, w2, w3;
-        if constexpr (kFull) {
-            // One unaligned 8-byte read (measured faster in this layout; the
-            // last two bytes, unused, lie inside the console's block).
-            std::uint64_t wq;
-            __builtin_memcpy(&wq, lds + wb, 8);
-            const std::uint32_t wlo = static_cast<std::uint32_t>(wq), whi = static_cast<std::uint32_t>(wq >> 32);
-            o2 = wlo & 0xFF; o1 = (wlo >> 8) & 0xFF; o0 = (wlo >> 16) & 0xFF;
-            w1 = wlo >> 24; w2 = whi & 0xFF; w3 = (whi >> 8) & 0xFF;
-        } else {
-            o2 = lds[wb]; o1 = lds[wb + 1]; o0 = lds[wb + 2];
-            w1 = lds[wb + 3]; w2 = lds[wb + 4]; w3 = lds[wb + 5];
-        }
+        // One unaligned 8-byte read; the last two bytes, unused, lie inside
+        // the console's block (or its spare and register bytes).
+        std::uint64_t wq;
+        __builtin_memcpy(&wq, lds + wb, 8);
+        const std::uint32_t wlo = static_cast<std::uint32_t>(wq), whi = static_cast<std::uint32_t>(wq >> 32);
+        const std::uint32_t o2 = wlo & 0xFF, o1 = (wlo >> 8) & 0xFF, o0 = (wlo >> 16) & 0xFF;
+        const std::uint32_t w1 = wlo >> 24, w2 = whi & 0xFF, w3 = (whi >> 8) & 0xFF;
 
         // Effective address and the operand candidates in LDS.
         const std::uint32_t abs = b1 | (b2 << 8);
@@ -706,16 +700,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         std::uint32_t op_n, b1_n, b2_n;
         {
             const std::uint32_t off = next & 0x7FFF;
-            if constexpr (kFull) {
-                // One unaligned 4-byte read (measured faster in this layout;
-                // the fourth byte, unused, may lie past the PRG image in the
-                // microcode area).
-                std::uint32_t ins;
-                __builtin_memcpy(&ins, lds + off, 4);
-                op_n = ins & 0xFF; b1_n = (ins >> 8) & 0xFF; b2_n = (ins >> 16) & 0xFF;
-            } else {
-                op_n = lds[off]; b1_n = lds[off + 1]; b2_n = lds[off + 2];
-            }
+            // One unaligned 4-byte read; the fourth byte, unused, may lie
+            // past the PRG image in the microcode area.
+            std::uint32_t ins;
+            __builtin_memcpy(&ins, lds + off, 4);
+            op_n = ins & 0xFF; b1_n = (ins >> 8) & 0xFF; b2_n = (ins >> 16) & 0xFF;
         }
 
         // Pushed bytes in window order (SP-2, SP-1, SP), merged with the old
@@ -766,14 +755,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
 
         // Memory writes: the stack window (pushed or old bytes), then the
         // operand to LDS (non-writers store to their spare byte).
-        if constexpr (kFull) {
-            // One unaligned 4-byte write: the window bytes and SP+1 as read.
+        {   // one unaligned 4-byte write: the window bytes and SP+1 as read
             const std::uint32_t win4 = (win & 0xFFFFFFu) | (w1 << 24);
             __builtin_memcpy(lds + wb, &win4, 4);
-        } else {
-            lds[wb] = static_cast<std::uint8_t>(win);
-            lds[wb + 1] = static_cast<std::uint8_t>(win >> 8);
-            lds[wb + 2] = static_cast<std::uint8_t>(win >> 16);
         }
         const std::uint32_t waddr = (wr && ram_lds) ? ram_a : spare;
         lds[waddr] = static_cast<std::uint8_t>(r);
