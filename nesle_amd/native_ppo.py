@@ -10,9 +10,10 @@ one stream:
 * the batch runs on PyTorch's current stream (``CudaBatch.set_stream``), so
   policy kernels, the step kernel and the RAM transpose are ordered without
   host synchronisation;
-* done consoles are restored by the step kernel's fused auto-reset (the
-  reference calls ``reset_envs`` with a host mask after a ``done.any()`` host
-  read every step, native_ppo.py:498-507); the RAM view after the step shows
+* done consoles are restored by the step's auto-reset, a restore kernel on
+  the same stream right after the step kernel (the reference calls
+  ``reset_envs`` with a host mask after a ``done.any()`` host read every
+  step, native_ppo.py:498-507); the RAM view after the step shows
   the post-reset state for them, exactly what the reference's
   ``reset_envs`` + ``ram_device`` sequence returns;
 * episode-length timeouts (``max_episode_steps``) reset through a device

@@ -113,7 +113,7 @@ def test_full_size_sampled_envs(num_envs, steps):
 def test_snapshot_autoreset_xdelta_reward():
     """Config 3 in miniature: 8 snapshots captured after seeded warm-up frames,
     done byte patched so episodes end within the run, x-delta reward with time
-    penalty, fused auto-reset; rewards, dones and post-reset states equal the
+    penalty, auto-reset; rewards, dones and post-reset states equal the
     oracle restoring the same snapshot."""
     rom_info = synthrom.make_rom(5)
     rom = rom_info.rom
@@ -158,7 +158,7 @@ def test_snapshot_autoreset_xdelta_reward():
 def test_benchmark_configuration_full_size_sampled():
     """The benchmark's configuration at full size: 65,536 consoles (RAM rows
     split between LDS and HBM), 8 snapshot levels spread at random, x-delta
-    reward with time penalty and fused auto-reset.  Sampled consoles (edges of
+    reward with time penalty and auto-reset.  Sampled consoles (edges of
     waves, workgroups and XCD ranges, random ones) have the rewards and dones
     of the oracle restoring the same snapshot after every step, and its state
     every third step; episodes end within the run."""

@@ -1,6 +1,6 @@
 """The GPU-resident PPO loop (nesle_amd.native_ppo) on the HIP batch: every
 rollout step's actions, rewards and done flags equal the oracle consoles
-stepped with the same controller masks, with the fused snapshot auto-reset
+stepped with the same controller masks, with the snapshot auto-reset
 and the episode-length timeout reset applied the same way; the update runs
 and changes the policy."""
 
