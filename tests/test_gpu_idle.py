@@ -39,25 +39,30 @@ def idle_rom() -> bytes:
     return nrom_bytes(2, code={0x8000: RESET, 0x9000: NMI}, reset=0x8000, nmi=0x9000, irq=0x8000)
 
 
-@pytest.mark.parametrize("frameskip,budget", [(1, 200000), (4, 200000), (2, 3000)])
-def test_idle_loop_fast_forward_matches_oracle(frameskip, budget):
+@pytest.mark.parametrize("n,frameskip,budget", [(64, 1, 200000), (64, 4, 200000), (64, 2, 3000),
+                                                 (16384, 4, 200000), (16384, 2, 3000)])
+def test_idle_loop_fast_forward_matches_oracle(n, frameskip, budget):
+    """64 consoles (all RAM in LDS, every console checked) and 16,384
+    (RAM split between LDS and HBM, sampled consoles)."""
     rom = idle_rom()
-    n, steps = 64, 12
-    say(f"[gpu] idle loop: N={n} fs={frameskip} budget={budget} steps={steps}")
+    steps = 12
+    rng = np.random.default_rng(n)
+    envs = list(range(n)) if n <= 64 else sorted({0, 63, 64, 255, 256, n - 1, *rng.integers(0, n, 26).tolist()})
+    say(f"[gpu] idle loop: N={n} fs={frameskip} budget={budget} steps={steps} checked={len(envs)}")
     b = abi.Batch(rom, n, frameskip=frameskip, max_instructions_per_frame=budget)
-    cons = [O.Oracle(rom) for _ in range(n)]
+    cons = [O.Oracle(rom) for _ in envs]
     for c in cons:
         c.set_reward()
     for k in range(steps):
         m = masks_for(4242, n, k)
         b.set_actions(m)
         b.step(stats_mode=1)
-        want = [c.step(int(m[e]), frameskip, budget) for e, c in enumerate(cons)]
-        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS), [w[0] for w in want], err_msg=f"step {k}")
-        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS), np.array([w[1] for w in want], np.float32))
+        want = [c.step(int(m[e]), frameskip, budget) for e, c in zip(envs, cons)]
+        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS)[envs], [w[0] for w in want], err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[envs], np.array([w[1] for w in want], np.float32))
         if k % 4 == 3:
-            for e, c in enumerate(cons):
+            for e, c in zip(envs, cons):
                 got, ref = b.save_state(e), c.save()
                 assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
-    ins = b.host(abi.VIEW_INSTRUCTIONS)
+    ins = b.host(abi.VIEW_INSTRUCTIONS)[envs]
     assert ins.min() != ins.max()   # consoles idled for different spans
