@@ -357,11 +357,11 @@ def test_full_size_snapshot_reset_properties():
     np.testing.assert_array_equal(a.host(abi.VIEW_RAM), after)
 
 
-def test_profile_counts_match_instructions():
+@pytest.mark.parametrize("n", [128, 16384])
+def test_profile_counts_match_instructions(n):
     """step_profile's opcode histogram sums to the per-console instruction
-    counts; only official opcodes appear."""
+    counts; only official opcodes appear (both LDS layouts)."""
     rom = _rom(4)
-    n = 128
     say(f"[gpu] profile: N={n}")
     b = abi.Batch(rom, n, frameskip=4)
     b.set_actions(masks_for(1, n, 0))
