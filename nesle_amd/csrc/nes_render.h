@@ -11,19 +11,31 @@ namespace render {
 constexpr int kPrecision = 22;             // Pillow's 8-bit resample fixed point
 constexpr std::uint32_t kOut = 84;         // gray observation is kOut x kOut
 constexpr std::uint32_t kHTaps = 9;        // 256 -> 84: ceil(256 / 84) * 2 + 1
-constexpr std::uint32_t kVTaps = 7;        // 240 -> 84: ceil(240 / 84) * 2 + 1
+constexpr std::uint32_t kVTaps = 8;        // 240 -> 84: ceil(240 / 84) * 2 + 1 = 7, padded to 8
+// Inputs an output actually reads: a BILINEAR window spans at most
+// 2 * scale + 1 inputs, 7.1 across (256 / 84) and 6.7 down (240 / 84), so
+// 8 consecutive inputs hold every window; the kernel reads 8 bytes per output.
+constexpr std::uint32_t kWindow = 8;
 
-// Per output column (h_) and row (v_): first input, input count, weights.
-struct Taps {
-    std::int32_t h_lo[kOut], h_n[kOut], h_k[kOut][kHTaps];
-    std::int32_t v_lo[kOut], v_n[kOut], v_k[kOut][kVTaps];
+// Pillow BILINEAR weights of one axis: per output column or row, first
+// input, input count, weights (each in [0, 2^22], exact in 24-bit products;
+// zero past the count).
+template <std::uint32_t kTaps>
+struct Axis {
+    std::int32_t lo[kOut], n[kOut], k[kOut][kTaps];
+};
+
+// The part of the tables the render kernel keeps in LDS.
+struct Staged {
+    Axis<kVTaps> v;          // 240 rows -> 84
+    std::uint8_t gray[64];   // gray level of each palette colour
+    std::uint8_t rgb[192];   // the renderer's RGB palette (64 x 3)
 };
 
 // Everything the render kernel looks up, uploaded once per batch.
 struct Tables {
-    Taps taps;               // Pillow BILINEAR weights for 256x240 -> 84x84
-    std::uint8_t gray[64];   // gray level of each palette colour
-    std::uint8_t rgb[192];   // the renderer's RGB palette (64 x 3)
+    Axis<kHTaps> h;          // 256 columns -> 84, read once per thread
+    Staged s;
 };
 
 // Host: the resize weights of Pillow's BILINEAR filter (libImaging/Resample.c

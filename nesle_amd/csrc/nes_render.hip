@@ -14,18 +14,31 @@
 // then Pillow's BILINEAR resize to 84x84; the host computes its fixed-point
 // weights (nes_render.h).
 //
-// One workgroup of 256 threads renders one console in bands of 8 rows.  A
-// thread owns 8 adjacent pixels of one row: it decodes the (at most two)
-// background tiles under them once -- nametable byte, attribute, both pattern
-// planes -- and then each sprite of the row that overlaps them once, so a
-// tile fetch serves 8 pixels.  Full-size outputs are written as 8-byte runs
-// (coalesced across the 32 threads of a row); the band's gray levels feed the
-// horizontal resample pass in LDS and the vertical pass runs once the
-// 240 x 84 intermediate is complete.  Pattern tables (8 KB, shared by every
-// console) are staged in LDS per workgroup, zero-filled for CHR RAM.
+// One workgroup of 256 threads renders one console in bands of 8 rows, in
+// three phases per band:
+//  1. background: a thread owns 8 adjacent pixels of one row.  It reads the
+//     (at most two) tiles under them -- nametable byte, attribute, both
+//     pattern planes in one 16-bit read -- and turns each pixel's colour
+//     index and tile into a byte selector, so that one v_perm over the two
+//     tiles' palette words yields 4 display values (and one more 4 gray
+//     levels);
+//  2. sprites: the sprites that meet the band are compacted by a ballot, and
+//     each (sprite, row) pair is one lane, which writes its opaque pixels as
+//     keys (OAM index, gray level, palette value) into the band's line buffer
+//     with an LDS atomic minimum -- the lowest OAM index wins, whatever the
+//     order;
+//  3. merge: a thread reads its 8 keys and replaces the background where a
+//     sprite key is present, all by byte permutes; it writes the full-size
+//     outputs as 8-byte runs (coalesced across the 32 threads of a row), and
+//     the band's gray levels feed the horizontal resample pass in LDS; the
+//     vertical pass runs once the intermediate rows an output row needs are
+//     complete.
+// Pattern tables (8 KB, shared by every console) are staged in LDS per
+// workgroup with the two planes of a tile row side by side, zeros for CHR RAM.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstddef>
 #include <cstdint>
 
 #include "nes_layout.h"
@@ -35,75 +48,98 @@ namespace nesle {
 namespace {
 
 constexpr std::uint32_t kThreads = 256;
+constexpr std::uint32_t kWaves = kThreads / 64;
 constexpr std::uint32_t kBand = 8;
 // Horizontally resampled rows kept for the vertical pass.  An output row is
 // emitted after the first band that completes its input window; windows are
 // at most 7 rows and end within the band, so no emitted row reaches back more
 // than 14 rows and the next band overwrites only rows no pending output needs.
 constexpr std::uint32_t kRing = 16;
+constexpr std::uint32_t kMidStride = 2 * kRing + 4;
+// Empty line-buffer entry; a sprite key is (OAM index << 16) | (gray << 8) |
+// palette value, always below it (bit 31 clear, value byte <= 0x3F).
+constexpr std::uint32_t kNoSprite = 0xFFFFFFFFu;
+// The tables are staged in 16-byte words and a row of vertical weights is
+// read as two of them.
+static_assert(offsetof(render::Tables, s) % 16 == 0 && sizeof(render::Staged) % 16 == 0, "tables staged in 16-byte words");
+static_assert(offsetof(render::Staged, v.k) % 16 == 0 && render::kVTaps == 8, "vertical weights: two 16-byte reads per row");
 
 // Scroll/ctrl pair one part of the frame is drawn with.
 struct View {
     std::uint32_t ctrl, sx, sy;
 };
 
-// Reverse the bit order of a byte (pattern rows are stored leftmost pixel in bit 7).
-__device__ __forceinline__ std::uint32_t rev8(std::uint32_t b) { return __builtin_bitreverse32(b) >> 24; }
-// Bits 0-7 of b to the even bits 0, 2, ..., 14.
-__device__ __forceinline__ std::uint32_t spread(std::uint32_t b) {
-    b = (b | (b << 4)) & 0x0F0Fu;
-    b = (b | (b << 2)) & 0x3333u;
-    return (b | (b << 1)) & 0x5555u;
+// v_perm_b32: byte i of the result is byte sel_i of the 8-byte value hi:lo
+// (0-3 lo, 4-7 hi; 8-11 replicate the sign bit of byte 1/3 of lo / hi; 12 zero).
+__device__ __forceinline__ std::uint32_t perm(std::uint32_t hi, std::uint32_t lo, std::uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// Bits 0-3 of n to bit 0 of bytes 0-3 (the four partial products do not overlap).
+__device__ __forceinline__ std::uint32_t spread4(std::uint32_t n) { return __umul24(n & 15u, 0x00204081u) & 0x01010101u; }
+// Byte selectors of 4 pixels: colour index from plane bits lo/hi (bits 0-3)
+// plus 4 where bit t is set (the second of two palette words).
+__device__ __forceinline__ std::uint32_t selectors(std::uint32_t lo, std::uint32_t hi, std::uint32_t t) {
+    return spread4(lo) | (spread4(hi) << 1) | (spread4(t) << 2);
 }
 
+// The two tiles under an 8-pixel window: pattern planes of the tile pair,
+// pixel p (0..15, left to right) at bit p (low plane) and bit 16 + p (high
+// plane); both tiles' attribute palettes; the window's offset into the pair.
+struct TilePair {
+    std::uint32_t planes, pal0, pal1, fx;
+};
+
 struct Console {
-    const std::uint8_t* chr;   // LDS, 8 KB pattern tables
-    const std::uint8_t* nt;    // LDS, snapshot nametable RAM
-    const std::uint8_t* oam;   // LDS, snapshot OAM
-    const std::uint8_t* pv;    // LDS, 32 palette values (aliases and grayscale applied)
+    const std::uint16_t* chr;   // LDS, pattern table rows: low plane | high plane << 8
+    const std::uint8_t* nt;     // LDS, snapshot nametable RAM
     std::uint32_t mask;
     // Nametable n = x | y << 1 lives at (x * mx + y * my) * 0x400 of nametable
     // RAM: vertical mirroring mx = 1, my = 0; horizontal 0, 1; four-screen 1, 2.
     std::uint32_t mx, my;
 
-    // Background of pixels x0..x0+7 of row y: palette values (0 = transparent)
-    // packed 8 bits per pixel, two words.  batch_background_color
-    // (batch_render.cuh:219-262) for each pixel, with one fetch per tile.
-    __device__ void background(const View& w, std::uint32_t x0, std::uint32_t y, std::uint32_t out[2]) const {
-        out[0] = out[1] = 0;
-        if (!(mask & 0x08)) return;
-        const std::uint32_t wy = w.sy + y;
-        const std::uint32_t coarse_y = (wy % 240) >> 3, fine_y = wy & 7;
-        const std::uint32_t nt_y = (((w.ctrl & 3) >> 1) + wy / 240) & 1;
-        const std::uint32_t pbase = (w.ctrl & 0x10) ? 0x1000u : 0u;
-        const std::uint32_t wx0 = w.sx + x0, fx = wx0 & 7;
-        std::uint32_t planes = 0, pal = 0;   // 16 pattern pixels (2 bits each), 2 attribute selects
+    // batch_background_color (batch_render.cuh:219-262) for the window
+    // x..x+7 of row y: the frame is a 512 x 480 world of 2 x 2 nametables,
+    // scrolled by (sx, sy) from the nametable ctrl selects, rows wrapping at 480.
+    __device__ TilePair tiles(const View& w, std::uint32_t x, std::uint32_t y) const {
+        std::uint32_t wy = w.sy + y + ((w.ctrl & 2) ? 240u : 0u);
+        if (wy >= 480) wy -= 480;
+        const std::uint32_t ty = wy >> 3, fine_y = wy & 7;
+        const bool lower = ty >= 30;
+        const std::uint32_t cy = lower ? ty - 30 : ty;
+        const std::uint32_t row = (lower ? my << 10 : 0u) + cy * 32;
+        const std::uint32_t arow = (lower ? my << 10 : 0u) + 0x3C0 + (cy >> 2) * 8;
+        const std::uint32_t ashift = (cy & 2) << 1;
+        const std::uint32_t wx = w.sx + x + ((w.ctrl & 1) ? 256u : 0u);
+        const std::uint32_t pt = (w.ctrl & 0x10) ? 256u : 0u;
+        std::uint32_t pat[2], pal[2];
         for (std::uint32_t k = 0; k < 2; ++k) {
-            const std::uint32_t wt = (wx0 >> 3) + k;                  // world tile column 0..63
-            const std::uint32_t coarse_x = wt & 31;
-            const std::uint32_t nt_x = ((w.ctrl & 1) + (wt >> 5)) & 1;
-            const std::uint8_t* n = nt + (nt_x * mx + nt_y * my) * 0x400;
-            const std::uint32_t tile = n[coarse_y * 32 + coarse_x];
-            const std::uint32_t lo = chr[(pbase + tile * 16 + fine_y) & 0x1FFF];
-            const std::uint32_t hi = chr[(pbase + tile * 16 + fine_y + 8) & 0x1FFF];
-            const std::uint32_t attr = n[0x3C0 + (coarse_y >> 2) * 8 + (coarse_x >> 2)];
-            const std::uint32_t shift = ((coarse_y & 2) << 1) | (coarse_x & 2);
-            // Interleave the planes: pixel j of the tile (bit 7 - j of each
-            // plane) at bits 2j..2j+1.
-            planes |= (spread(rev8(lo)) | (spread(rev8(hi)) << 1)) << (16 * k);
-            pal |= ((attr >> shift) & 3) << (2 * k);
+            const std::uint32_t tx = ((wx >> 3) + k) & 63, cx = tx & 31;
+            const std::uint32_t ntx = (tx & 32) ? mx << 10 : 0u;
+            const std::uint32_t tile = nt[row + ntx + cx];
+            const std::uint32_t attr = nt[arow + ntx + (cx >> 2)];
+            pal[k] = (attr >> (ashift | (cx & 2))) & 3;
+            pat[k] = chr[(pt + tile) * 8 + fine_y];
         }
-        // The 4 palette values of each tile's attribute, colour 0 cleared
-        // (transparent); pixel i of the run is pixel fx + i of the pair.
-        const std::uint32_t* pw = reinterpret_cast<const std::uint32_t*>(pv);
-        const std::uint32_t p0 = pw[pal & 3] & ~0xFFu, p1 = pw[(pal >> 2) & 3] & ~0xFFu;
-        const std::uint32_t run = planes >> (2 * fx);
-        for (std::uint32_t i = 0; i < 8; ++i) {
-            const std::uint32_t c = (run >> (2 * i)) & 3;
-            const std::uint32_t v = ((i + fx < 8 ? p0 : p1) >> (8 * c)) & 0xFF;
-            out[i >> 2] |= v << (8 * (i & 3));
-        }
-        if (!(mask & 0x02) && x0 == 0) out[0] = out[1] = 0;   // left 8 pixels hidden
+        // Bit-reverse the word [lo0, hi0, lo1, hi1] to [rhi1, rlo1, rhi0, rlo0]
+        // and reorder to [rlo0, rlo1, rhi0, rhi1]: leftmost pixel at bit 0.
+        const std::uint32_t r = __builtin_bitreverse32(pat[0] | (pat[1] << 16));
+        return {perm(r, r, 0x00020103u), pal[0], pal[1], wx & 7};
+    }
+
+    // Opacity (bit i: pixel x + i) of the background of the window x..x+7
+    // of row y: colour index not 0 and palette value not 0, nothing where the
+    // background is off or hidden in the left column.
+    __device__ std::uint32_t opacity(const View& w, std::uint32_t x, std::uint32_t y, const std::uint32_t* bgo) const {
+        if (!(mask & 0x08)) return 0;
+        const TilePair p = tiles(w, x, y);
+        const std::uint32_t lo = p.planes >> p.fx, hi = p.planes >> (p.fx + 16), t = 0xFF00u >> p.fx;
+        const std::uint32_t a = bgo[p.pal0], b = bgo[p.pal1];
+        // Opacity bytes (0 or 1) of pixels 0-3 and 4-7, gathered to 4 bits each.
+        const std::uint32_t o0 = perm(b, a, selectors(lo, hi, t)) * 0x01020408u >> 24;
+        const std::uint32_t o1 = perm(b, a, selectors(lo >> 4, hi >> 4, t >> 4)) * 0x01020408u >> 24;
+        std::uint32_t o = o0 | (o1 << 4);
+        if (!(mask & 0x02) && x < 8) o &= (0xFF00u >> x) & 0xFFu;
+        return o;
     }
 };
 
@@ -111,43 +147,100 @@ __device__ __forceinline__ std::uint32_t byte_of(const std::uint32_t w[2], std::
     return (w[i >> 2] >> (8 * (i & 3))) & 0xFF;
 }
 
+// Pillow's fixed-point sum of 8 consecutive 8-bit inputs (bytes of w) with
+// weights k (each in [0, 2^22], so 24-bit products are exact), rounded.
+__device__ __forceinline__ std::int32_t window8(const uint2 w, const std::int32_t k[8]) {
+    std::int32_t acc = 1 << (render::kPrecision - 1);
+    for (std::uint32_t j = 0; j < 4; ++j) acc += __mul24(static_cast<std::int32_t>((w.x >> (8 * j)) & 0xFF), k[j]);
+    for (std::uint32_t j = 0; j < 4; ++j) acc += __mul24(static_cast<std::int32_t>((w.y >> (8 * j)) & 0xFF), k[4 + j]);
+    return acc;
+}
+
 __device__ __forceinline__ std::uint32_t clip8(std::int32_t acc) {
     const std::int32_t v = acc >> render::kPrecision;
     return static_cast<std::uint32_t>(v < 0 ? 0 : (v > 255 ? 255 : v));
 }
 
+// Sprite pixels of 4 line-buffer keys over background words: display
+// values d and gray levels g of the 4 pixels, background where no key.
+__device__ __forceinline__ void merge(const uint4 k, std::uint32_t& d, std::uint32_t& g) {
+    const std::uint32_t t = perm(k.y, k.x, 0x05010400u);        // [v0, v1, g0, g1]
+    const std::uint32_t u = perm(k.w, k.z, 0x05010400u);        // [v2, v3, g2, g3]
+    const std::uint32_t v = perm(u, t, 0x05040100u);            // values
+    const std::uint32_t gr = perm(u, t, 0x07060302u);           // gray levels
+    // 0xFF where the value byte is 0xFF (no key), from the bytes' sign bits.
+    const std::uint32_t none = perm(v << 8, v, 0x090B080Au);
+    d = (none & d) | (~none & v);
+    g = (none & g) | (~none & gr);
+}
+
 __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
-    __shared__ __attribute__((aligned(16))) std::uint8_t chr[8192];
+    __shared__ __attribute__((aligned(16))) std::uint16_t chr[4096];          // [512 tiles][8 rows]
     __shared__ __attribute__((aligned(16))) std::uint8_t rec[present::kMaxBytes];
-    __shared__ std::uint64_t rows[240];
-    __shared__ __attribute__((aligned(16))) std::uint8_t gband[kBand][256];
-    __shared__ std::uint8_t mid[kRing][render::kOut];
-    __shared__ __attribute__((aligned(16))) render::Tables tab;
-    __shared__ __attribute__((aligned(4))) std::uint8_t pv[32];
+    __shared__ __attribute__((aligned(16))) std::uint32_t line[kBand][256];   // sprite keys of the band
+    __shared__ __attribute__((aligned(16))) std::uint8_t gband[2][kBand][256];   // gray rows of the last two bands
+    // Horizontally resampled rows, column-major, the ring stored twice so an
+    // output's window (kWindow rows from any ring position) is contiguous; a
+    // column takes 9 dwords, so the 64 columns a wave touches fall in
+    // distinct LDS banks.
+    __shared__ __attribute__((aligned(16))) std::uint8_t mid[render::kOut][kMidStride];
+    __shared__ __attribute__((aligned(16))) render::Staged tab;
+    __shared__ uint2 bgw[4];          // background palettes: display values, gray levels
+    __shared__ uint2 spw[4];          // sprite palettes: palette values, gray levels
+    __shared__ std::uint32_t bgo[4];  // background palettes: 1 where opaque
+    __shared__ std::uint8_t list[kWaves][64];   // per wave: sprites that meet the band
 
     const std::uint32_t tid = threadIdx.x, env = blockIdx.x;
     {
         const uint4* src = reinterpret_cast<const uint4*>(a.present + static_cast<std::size_t>(env) * a.present_stride);
         for (std::uint32_t i = tid; i < a.present_stride / 16; i += kThreads) reinterpret_cast<uint4*>(rec)[i] = src[i];
         // Pattern tables: the CHR ROM (an image smaller than 8 KB repeats), or
-        // zeros for CHR RAM, which the batched renderer reads as 0.
+        // zeros for CHR RAM, which the batched renderer reads as 0.  A tile's
+        // 16 bytes (8 low-plane rows, 8 high-plane rows) become 8 row pairs.
         const std::uint32_t words = a.chr_size / 16;
         const uint4* c = reinterpret_cast<const uint4*>(a.chr);
-        for (std::uint32_t i = tid; i < 8192 / 16; i += kThreads)
-            reinterpret_cast<uint4*>(chr)[i] = words != 0 ? c[i % words] : make_uint4(0, 0, 0, 0);
-        const std::uint32_t* t = reinterpret_cast<const std::uint32_t*>(a.tables);
-        for (std::uint32_t i = tid; i < sizeof(render::Tables) / 4; i += kThreads)
-            reinterpret_cast<std::uint32_t*>(&tab)[i] = t[i];
+        for (std::uint32_t i = tid; i < 512; i += kThreads) {
+            const uint4 t = words != 0 ? c[i % words] : make_uint4(0, 0, 0, 0);
+            reinterpret_cast<uint4*>(chr)[i] = make_uint4(perm(t.z, t.x, 0x05010400u), perm(t.z, t.x, 0x07030602u),
+                                                          perm(t.w, t.y, 0x05010400u), perm(t.w, t.y, 0x07030602u));
+        }
+        const uint4* t = reinterpret_cast<const uint4*>(&a.tables->s);
+        for (std::uint32_t i = tid; i < sizeof(render::Staged) / 16; i += kThreads) reinterpret_cast<uint4*>(&tab)[i] = t[i];
+        for (std::uint32_t i = tid; i < kBand * 256 / 4; i += kThreads)
+            reinterpret_cast<uint4*>(line)[i] = make_uint4(kNoSprite, kNoSprite, kNoSprite, kNoSprite);
     }
     __syncthreads();
 
     const std::uint32_t mask = rec[present::kMask];
     const std::uint8_t* oam = rec + present::kOam;
-    if (tid < 32) {   // batch_palette_value: aliases of $3F10/14/18/1C, grayscale, 6 bits
-        const std::uint32_t i = ((tid & 0x13) == 0x10) ? (tid & 0x0F) : tid;
-        std::uint32_t v = rec[present::kPalette + i];
-        if (mask & 0x01) v &= 0x30;
-        pv[tid] = static_cast<std::uint8_t>(v & 0x3F);
+    if (tid < 8) {
+        // batch_palette_value: aliases of $3F10/14/18/1C, grayscale, 6 bits.
+        auto value = [&](std::uint32_t i) {
+            std::uint32_t v = rec[present::kPalette + (((i & 0x13) == 0x10) ? (i & 0x0F) : i)];
+            if (mask & 0x01) v &= 0x30;
+            return v & 0x3F;
+        };
+        const std::uint32_t q = tid & 3;
+        std::uint32_t v = 0, g = 0, o = 0;
+        for (std::uint32_t c = 0; c < 4; ++c) {
+            std::uint32_t p;
+            if (tid < 4) {   // background: colour 0 and value 0 show the backdrop and are transparent
+                p = value(4 * q + c);
+                const bool opaque = c != 0 && p != 0;
+                if (!opaque) p = value(0);
+                o |= (opaque ? 1u : 0u) << (8 * c);
+            } else {
+                p = value(16 + 4 * q + c);
+            }
+            v |= p << (8 * c);
+            g |= static_cast<std::uint32_t>(tab.gray[p]) << (8 * c);
+        }
+        if (tid < 4) {
+            bgw[q] = make_uint2(v, g);
+            bgo[q] = o;
+        } else {
+            spw[q] = make_uint2(v, g);
+        }
     }
     // resolve_render_env_views (batch_render.cuh:336-366).
     View play{rec[present::kCtrlEnd], rec[present::kSxEnd], rec[present::kSyEnd]};
@@ -158,129 +251,158 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
         split = 0;
     }
     const std::uint32_t height = (play.ctrl & 0x20) ? 16 : 8;
-    if (tid < 240) {   // sprites covering each row, by OAM index
-        std::uint64_t m = 0;
-        for (std::uint32_t s = 0; s < 64; ++s) {
-            const std::uint32_t dy = tid - (static_cast<std::uint32_t>(oam[4 * s]) + 1);
-            m |= (dy < height ? 1ull : 0ull) << s;
-        }
-        rows[tid] = (mask & 0x10) ? m : 0ull;
-    }
     __syncthreads();
 
-    Console con{chr, rec + present::kNametable, oam, pv, mask, a.nt_mode == 1 ? 0u : 1u,
-                a.nt_mode == 2 ? 2u : a.nt_mode == 1 ? 1u : 0u};
+    const Console con{chr, rec + present::kNametable, mask, a.nt_mode == 1 ? 0u : 1u,
+                      a.nt_mode == 2 ? 2u : a.nt_mode == 1 ? 1u : 0u};
     const std::uint32_t r = tid >> 5, x0 = (tid & 31) * 8;
-    const std::uint32_t backdrop = pv[0];
+    const std::uint32_t lane = tid & 63, wave = tid >> 6;
+    const std::uint32_t backdrop = bgw[0].x & 0xFF, backdrop_gray = bgw[0].y & 0xFF;
+    const bool bg_on = (mask & 0x08) && (x0 != 0 || (mask & 0x02));   // else this run shows the backdrop
+    const bool clip = !(mask & 0x04);                                  // sprites hidden in the left column
     std::uint32_t next_oy = 0;   // first gray row not yet written
-    // Horizontal resample: thread t < 252 owns output column t % 84 for band
-    // rows t / 84, +3, +6, with that column's weights in registers (taps past
-    // the window's end carry weight 0 and read inside the row).
+    // Resample passes: thread t < 252 owns output column t % 84, for band rows
+    // t / 84, +3, +6 of the horizontal pass and output rows t / 84, +3, ... of
+    // the vertical pass.  The column's horizontal weights sit in registers,
+    // over the 8 inputs from h_lo (taps past the window's end weigh 0 and
+    // read inside the row).
     const std::uint32_t h_rows = tid < 3 * render::kOut ? 1u : 0u;
     const std::uint32_t h_ox = tid % render::kOut, h_r0 = tid / render::kOut;
-    std::int32_t h_k[render::kHTaps];
-    std::uint32_t h_lo = tab.taps.h_lo[h_ox];
-    if (h_lo + render::kHTaps > 256) h_lo = 256 - render::kHTaps;
-    for (std::uint32_t j = 0; j < render::kHTaps; ++j) {
-        const std::int32_t k = static_cast<std::int32_t>(j + h_lo) - tab.taps.h_lo[h_ox];   // tap index of input h_lo + j
-        h_k[j] = (k >= 0 && k < tab.taps.h_n[h_ox]) ? tab.taps.h_k[h_ox][k] : 0;
+    std::int32_t h_k[render::kWindow];
+    const render::Axis<render::kHTaps>& ht = a.tables->h;
+    const std::int32_t first = ht.lo[h_ox], taps = ht.n[h_ox];
+    const std::uint32_t h_lo = first + render::kWindow > 256 ? 256 - render::kWindow : first;
+    for (std::uint32_t j = 0; j < render::kWindow; ++j) {
+        const std::int32_t k = static_cast<std::int32_t>(j + h_lo) - first;   // tap index of input h_lo + j
+        h_k[j] = (k >= 0 && k < taps) ? ht.k[h_ox][k] : 0;
     }
-    for (std::uint32_t y0 = 0; y0 < 240; y0 += kBand) {
-        const std::uint32_t y = y0 + r;
-        const bool upper = static_cast<std::int32_t>(y) < split;
-        std::uint32_t bg[2];
-        con.background(upper ? hud : play, x0, y, bg);
-        std::uint32_t out[2] = {0, 0};
-        for (std::uint32_t i = 0; i < 8; ++i) {
-            const std::uint32_t v = byte_of(bg, i);
-            out[i >> 2] |= (v != 0 ? v : backdrop) << (8 * (i & 3));
-        }
-        // Sprites, lowest OAM index first (batch_render.cuh:264-330).
-        std::uint64_t m = rows[y];
-        std::uint32_t done = ((mask & 0x04) || x0 >= 8) ? 0u : 0xFFu;   // left-column clipping
-        bool have_play_bg = !upper;
-        std::uint32_t play_bg[2] = {bg[0], bg[1]};
-        while (m != 0 && done != 0xFF) {
-            const std::uint32_t s = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(m)) - 1);
-            m &= m - 1;
-            const std::uint32_t sxp = oam[4 * s + 3];
-            const std::uint32_t off = x0 + 8 - sxp;   // sprite column of pixel i is i + x0 - sxp
-            if (off - 1 >= 15) continue;              // no overlap with x0..x0+7
-            const std::uint32_t attr = oam[4 * s + 2], tile = oam[4 * s + 1];
-            std::uint32_t py = y - (oam[4 * s] + 1u);
-            std::uint32_t addr;
-            if (play.ctrl & 0x20) {
-                if (attr & 0x80) py = 15 - py;
-                addr = ((tile & 1) ? 0x1000u : 0u) + (((tile & 0xFE) + (py >> 3)) & 0xFF) * 16 + (py & 7);
-            } else {
-                if (attr & 0x80) py = 7 - py;
-                addr = ((play.ctrl & 0x08) ? 0x1000u : 0u) + tile * 16 + py;
-            }
-            std::uint32_t lo = chr[addr & 0x1FFF], hi = chr[(addr + 8) & 0x1FFF];
-            if (attr & 0x40) {
-                lo = rev8(lo);
-                hi = rev8(hi);
-            }
-            if ((attr & 0x20) && !have_play_bg) {   // behind: opacity of the frame-end view
-                con.background(play, x0, y, play_bg);
-                have_play_bg = true;
-            }
-            const std::uint32_t base = 0x10 + (attr & 3) * 4;
-            for (std::uint32_t i = 0; i < 8; ++i) {
-                const std::uint32_t px = i + x0 - sxp;
-                if (px >= 8 || ((done >> i) & 1)) continue;
-                const std::uint32_t bit = 7 - px;
-                const std::uint32_t sc = ((lo >> bit) & 1) | (((hi >> bit) & 1) << 1);
-                if (sc == 0 || ((attr & 0x20) && byte_of(play_bg, i) != 0)) continue;
-                const std::uint32_t sh = 8 * (i & 3);
-                out[i >> 2] = (out[i >> 2] & ~(0xFFu << sh)) | (static_cast<std::uint32_t>(pv[base + sc]) << sh);
-                done |= 1u << i;
-            }
-        }
-        const std::size_t pix = static_cast<std::size_t>(env) * 240 * 256 + y * 256 + x0;
-        if (a.palette) *reinterpret_cast<uint2*>(a.palette + pix) = make_uint2(out[0], out[1]);
-        if (a.rgb) {
-            std::uint32_t w[6] = {0, 0, 0, 0, 0, 0};
-            for (std::uint32_t i = 0; i < 8; ++i) {
-                const std::uint32_t c = byte_of(out, i);
-                for (std::uint32_t ch = 0; ch < 3; ++ch) {
-                    const std::uint32_t b = 3 * i + ch;
-                    w[b >> 2] |= static_cast<std::uint32_t>(tab.rgb[3 * c + ch]) << (8 * (b & 3));
+    // Band k is drawn in iteration k (background and sprites, then the merge)
+    // while iteration k + 1 resamples it (horizontal pass beside band k + 1's
+    // background and sprites, vertical pass beside its merge): two barriers a
+    // band.  The gray rows of a band alternate between two buffers.
+    constexpr std::uint32_t kBands = 240 / kBand;
+    for (std::uint32_t band = 0; band <= kBands; ++band) {
+        const bool draw = band < kBands, resample = a.gray && band > 0;
+        const std::uint32_t y0 = band * kBand, y = y0 + r;
+        std::uint32_t d[2], g[2];
+        if (draw) {
+            // 1. Background of the run: display values d (palette value 0 shows
+            // the backdrop) and their gray levels g.
+            d[0] = d[1] = backdrop * 0x01010101u;
+            g[0] = g[1] = backdrop_gray * 0x01010101u;
+            if (bg_on) {
+                const TilePair p = con.tiles(static_cast<std::int32_t>(y) < split ? hud : play, x0, y);
+                const std::uint32_t lo = p.planes >> p.fx, hi = p.planes >> (p.fx + 16), t = 0xFF00u >> p.fx;
+                const uint2 w0 = bgw[p.pal0], w1 = bgw[p.pal1];
+                for (std::uint32_t h = 0; h < 2; ++h) {
+                    const std::uint32_t sel = selectors(lo >> (4 * h), hi >> (4 * h), t >> (4 * h));
+                    d[h] = perm(w1.x, w0.x, sel);
+                    g[h] = perm(w1.y, w0.y, sel);
                 }
             }
-            uint2* o = reinterpret_cast<uint2*>(a.rgb + pix * 3);
-            o[0] = make_uint2(w[0], w[1]);
-            o[1] = make_uint2(w[2], w[3]);
-            o[2] = make_uint2(w[4], w[5]);
+            // 2. Sprites (batch_render.cuh:264-330) into the line buffer.
+            if (mask & 0x10) {
+                // Sprite `lane` covers rows oam[4 * lane] + 1 .. + height; the
+                // sprites meeting rows y0..y0+7, in OAM order, to this wave's list.
+                const std::uint32_t top = oam[4 * lane];
+                const bool meets = top + height - y0 < height + kBand - 1;
+                const std::uint64_t ball = __ballot(meets);
+                const std::uint32_t count = static_cast<std::uint32_t>(__popcll(ball));
+                if (meets)
+                    list[wave][__builtin_amdgcn_mbcnt_hi(static_cast<std::uint32_t>(ball >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<std::uint32_t>(ball), 0u))] =
+                        static_cast<std::uint8_t>(lane);
+                __builtin_amdgcn_wave_barrier();
+                for (std::uint32_t slot = tid; slot < count * kBand; slot += kThreads) {
+                    const std::uint32_t s = list[wave][slot / kBand], row = slot % kBand, sy = y0 + row;
+                    const std::uint32_t o = *reinterpret_cast<const std::uint32_t*>(oam + 4 * s);
+                    const std::uint32_t attr = (o >> 16) & 0xFF, tile = (o >> 8) & 0xFF, sx = o >> 24;
+                    std::uint32_t py = sy - ((o & 0xFF) + 1);
+                    if (py >= height) continue;
+                    std::uint32_t t;   // pattern tile 0..511
+                    if (height == 16) {
+                        if (attr & 0x80) py = 15 - py;
+                        t = ((tile & 1) << 8) + (((tile & 0xFE) + (py >> 3)) & 0xFF);
+                    } else {
+                        if (attr & 0x80) py = 7 - py;
+                        t = ((play.ctrl & 0x08) ? 256u : 0u) + tile;
+                    }
+                    std::uint32_t pat = chr[t * 8 + (py & 7)];
+                    if (!(attr & 0x40)) {   // not flipped: leftmost pixel to bit 0
+                        const std::uint32_t rv = __builtin_bitreverse32(pat);
+                        pat = perm(rv, rv, 0x0C0C0203u);
+                    }
+                    std::uint32_t op = (pat | (pat >> 8)) & 0xFF;   // bit j: column j opaque
+                    if (sx > 248) op &= 0xFFu >> (sx - 248);         // off the right edge
+                    if (clip && sx < 8) op &= (0xFF00u >> sx) & 0xFFu;
+                    if ((attr & 0x20) && op != 0) op &= ~con.opacity(play, sx, sy, bgo);   // behind the background
+                    if (op == 0) continue;
+                    const uint2 sp = spw[attr & 3];
+                    std::uint32_t* dst = &line[row][sx];
+                    for (std::uint32_t h = 0; h < 2; ++h) {
+                        const std::uint32_t sel = selectors(pat >> (4 * h), pat >> (8 + 4 * h), 0);
+                        for (std::uint32_t q = 0; q < 2; ++q) {
+                            // (value, gray) of columns 4h + 2q and 4h + 2q + 1.
+                            const std::uint32_t pair = perm(sp.y, sp.x, perm(sel, sel, 0x01010000u + 0x02020202u * q) + 0x04000400u);
+                            const std::uint32_t j = 4 * h + 2 * q;
+                            if ((op >> j) & 1) atomicMin(dst + j, (s << 16) | (pair & 0xFFFF));
+                            if ((op >> (j + 1)) & 1) atomicMin(dst + j + 1, (s << 16) | (pair >> 16));
+                        }
+                    }
+                }
+            }
         }
-        if (a.gray) {
-            std::uint32_t g[2] = {0, 0};
-            for (std::uint32_t i = 0; i < 8; ++i) g[i >> 2] |= static_cast<std::uint32_t>(tab.gray[byte_of(out, i)]) << (8 * (i & 3));
-            *reinterpret_cast<uint2*>(&gband[r][x0]) = make_uint2(g[0], g[1]);
-        }
-        __syncthreads();
-        if (a.gray && h_rows != 0) {   // horizontal pass of the band: column h_ox of rows h_r0, +3, +6
+        if (resample && h_rows != 0) {   // horizontal pass of the previous band: column h_ox of rows h_r0, +3, +6
             for (std::uint32_t rr = h_r0; rr < kBand; rr += 3) {
-                std::int32_t acc = 1 << (render::kPrecision - 1);
-                for (std::uint32_t j = 0; j < render::kHTaps; ++j) acc += gband[rr][h_lo + j] * h_k[j];
-                mid[(y0 + rr) % kRing][h_ox] = static_cast<std::uint8_t>(clip8(acc));
+                uint2 w;
+                __builtin_memcpy(&w, &gband[(band - 1) & 1][rr][h_lo], 8);   // unaligned 8-byte read
+                const std::uint32_t slot = (y0 - kBand + rr) % kRing;
+                mid[h_ox][slot] = mid[h_ox][slot + kRing] = static_cast<std::uint8_t>(clip8(window8(w, h_k)));
             }
         }
         __syncthreads();
-        if (a.gray) {   // vertical pass of every output row whose window is now complete
+        if (draw) {
+            // 3. Merge the run's sprite keys; the buffer is left empty for the next band.
+            {
+                uint4* keys = reinterpret_cast<uint4*>(&line[r][x0]);
+                merge(keys[0], d[0], g[0]);
+                merge(keys[1], d[1], g[1]);
+                keys[0] = keys[1] = make_uint4(kNoSprite, kNoSprite, kNoSprite, kNoSprite);
+            }
+            const std::size_t pix = static_cast<std::size_t>(env) * 240 * 256 + y * 256 + x0;
+            if (a.palette) *reinterpret_cast<uint2*>(a.palette + pix) = make_uint2(d[0], d[1]);
+            if (a.rgb) {
+                std::uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+                for (std::uint32_t i = 0; i < 8; ++i) {
+                    const std::uint32_t c = byte_of(d, i);
+                    for (std::uint32_t ch = 0; ch < 3; ++ch) {
+                        const std::uint32_t b = 3 * i + ch;
+                        w[b >> 2] |= static_cast<std::uint32_t>(tab.rgb[3 * c + ch]) << (8 * (b & 3));
+                    }
+                }
+                uint2* o = reinterpret_cast<uint2*>(a.rgb + pix * 3);
+                o[0] = make_uint2(w[0], w[1]);
+                o[1] = make_uint2(w[2], w[3]);
+                o[2] = make_uint2(w[4], w[5]);
+            }
+            if (a.gray) *reinterpret_cast<uint2*>(&gband[band & 1][r][x0]) = make_uint2(g[0], g[1]);
+        }
+        if (resample) {   // vertical pass of every output row whose window the previous band completed
             std::uint32_t end = next_oy;
-            while (end < render::kOut && static_cast<std::uint32_t>(tab.taps.v_lo[end] + tab.taps.v_n[end]) <= y0 + kBand)
+            while (end < render::kOut && static_cast<std::uint32_t>(tab.v.lo[end] + tab.v.n[end]) <= y0)
                 ++end;
             std::uint8_t* out = a.gray + static_cast<std::size_t>(env) * render::kOut * render::kOut;
-            for (std::uint32_t i = next_oy * render::kOut + tid; i < end * render::kOut; i += kThreads) {
-                const std::uint32_t oy = i / render::kOut, ox = i % render::kOut;
-                std::int32_t acc = 1 << (render::kPrecision - 1);
-                const std::uint32_t lo = tab.taps.v_lo[oy], n = tab.taps.v_n[oy];
-                for (std::uint32_t j = 0; j < n; ++j) acc += mid[(lo + j) % kRing][ox] * tab.taps.v_k[oy][j];
-                out[i] = static_cast<std::uint8_t>(clip8(acc));
+            for (std::uint32_t oy = next_oy + h_r0; h_rows != 0 && oy < end; oy += 3) {
+                uint2 w;
+                __builtin_memcpy(&w, &mid[h_ox][tab.v.lo[oy] % kRing], 8);   // unaligned 8-byte read
+                const int4* k = reinterpret_cast<const int4*>(tab.v.k[oy]);
+                const int4 k0 = k[0], k1 = k[1];
+                const std::int32_t kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                out[oy * render::kOut + h_ox] = static_cast<std::uint8_t>(clip8(window8(w, kv)));
             }
             next_oy = end;
         }
+        __syncthreads();
     }
 }
 
@@ -348,15 +470,15 @@ void axis(int in_size, std::int32_t* lo, std::int32_t* n, std::int32_t (*k)[kTap
 
 Tables make_tables() {
     Tables t{};
-    axis<kHTaps>(256, t.taps.h_lo, t.taps.h_n, t.taps.h_k);
-    axis<kVTaps>(240, t.taps.v_lo, t.taps.v_n, t.taps.v_k);
+    axis<kHTaps>(256, t.h.lo, t.h.n, t.h.k);
+    axis<kVTaps>(240, t.s.v.lo, t.s.v.n, t.s.v.k);
     // numpy's float luma of the RGB frame (an FMA chain over the channels),
     // truncated to uint8.
     for (std::uint32_t c = 0; c < 64; ++c) {
         const double r = kNesRgbHost[3 * c], g = kNesRgbHost[3 * c + 1], b = kNesRgbHost[3 * c + 2];
-        t.gray[c] = static_cast<std::uint8_t>(static_cast<int>(std::fma(b, 0.114, std::fma(g, 0.587, r * 0.299))));
+        t.s.gray[c] = static_cast<std::uint8_t>(static_cast<int>(std::fma(b, 0.114, std::fma(g, 0.587, r * 0.299))));
     }
-    for (std::uint32_t i = 0; i < 192; ++i) t.rgb[i] = kNesRgbHost[i];
+    for (std::uint32_t i = 0; i < 192; ++i) t.s.rgb[i] = kNesRgbHost[i];
     return t;
 }
 
