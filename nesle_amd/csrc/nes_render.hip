@@ -56,6 +56,7 @@ constexpr std::uint32_t kBand = 8;
 // than 14 rows and the next band overwrites only rows no pending output needs.
 constexpr std::uint32_t kRing = 16;
 constexpr std::uint32_t kMidStride = 2 * kRing + 4;
+constexpr std::uint32_t kGrayStride = 256 + 8;
 // Empty line-buffer entry; a sprite key is (OAM index << 16) | (gray << 8) |
 // palette value, always below it (bit 31 clear, value byte <= 0x3F).
 constexpr std::uint32_t kNoSprite = 0xFFFFFFFFu;
@@ -147,6 +148,15 @@ __device__ __forceinline__ std::uint32_t byte_of(const std::uint32_t w[2], std::
     return (w[i >> 2] >> (8 * (i & 3))) & 0xFF;
 }
 
+// Bytes p..p+7 of a 4-byte-aligned LDS row (p & ~3 plus 11 inside it): three
+// aligned dword reads and two byte funnel shifts (an unaligned 8-byte LDS
+// read costs the LDS pipeline several passes).
+__device__ __forceinline__ uint2 bytes8(const std::uint8_t* row, std::uint32_t p) {
+    const std::uint32_t* d = reinterpret_cast<const std::uint32_t*>(row + (p & ~3u));
+    const std::uint32_t d0 = d[0], d1 = d[1], d2 = d[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, p & 3), __builtin_amdgcn_alignbyte(d2, d1, p & 3));
+}
+
 // Pillow's fixed-point sum of 8 consecutive 8-bit inputs (bytes of w) with
 // weights k (each in [0, 2^22], so 24-bit products are exact), rounded.
 __device__ __forceinline__ std::int32_t window8(const uint2 w, const std::int32_t k[8]) {
@@ -178,7 +188,9 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
     __shared__ __attribute__((aligned(16))) std::uint16_t chr[4096];          // [512 tiles][8 rows]
     __shared__ __attribute__((aligned(16))) std::uint8_t rec[present::kMaxBytes];
     __shared__ __attribute__((aligned(16))) std::uint32_t line[kBand][256];   // sprite keys of the band
-    __shared__ __attribute__((aligned(16))) std::uint8_t gband[2][kBand][256];   // gray rows of the last two bands
+    // Gray rows of the last two bands (rows padded so a window's third dword
+    // stays inside its row).
+    __shared__ __attribute__((aligned(16))) std::uint8_t gband[2][kBand][kGrayStride];
     // Horizontally resampled rows, column-major, the ring stored twice so an
     // output's window (kWindow rows from any ring position) is contiguous; a
     // column takes 9 dwords, so the 64 columns a wave touches fall in
@@ -354,8 +366,7 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
         }
         if (resample && h_rows != 0) {   // horizontal pass of the previous band: column h_ox of rows h_r0, +3, +6
             for (std::uint32_t rr = h_r0; rr < kBand; rr += 3) {
-                uint2 w;
-                __builtin_memcpy(&w, &gband[(band - 1) & 1][rr][h_lo], 8);   // unaligned 8-byte read
+                const uint2 w = bytes8(gband[(band - 1) & 1][rr], h_lo);
                 const std::uint32_t slot = (y0 - kBand + rr) % kRing;
                 mid[h_ox][slot] = mid[h_ox][slot + kRing] = static_cast<std::uint8_t>(clip8(window8(w, h_k)));
             }
@@ -393,8 +404,7 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
                 ++end;
             std::uint8_t* out = a.gray + static_cast<std::size_t>(env) * render::kOut * render::kOut;
             for (std::uint32_t oy = next_oy + h_r0; h_rows != 0 && oy < end; oy += 3) {
-                uint2 w;
-                __builtin_memcpy(&w, &mid[h_ox][tab.v.lo[oy] % kRing], 8);   // unaligned 8-byte read
+                const uint2 w = bytes8(mid[h_ox], tab.v.lo[oy] % kRing);
                 const int4* k = reinterpret_cast<const int4*>(tab.v.k[oy]);
                 const int4 k0 = k[0], k1 = k[1];
                 const std::int32_t kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
