@@ -18,16 +18,36 @@ constexpr std::uint32_t kVTaps = 8;        // 240 -> 84: ceil(240 / 84) * 2 + 1 
 constexpr std::uint32_t kWindow = 8;
 
 // Pillow BILINEAR weights of one axis: per output column or row, first
-// input, input count, weights (each in [0, 2^22], exact in 24-bit products;
-// zero past the count).
+// input, input count, weights (each in [0, 2^22]; zero past the count).
 template <std::uint32_t kTaps>
 struct Axis {
     std::int32_t lo[kOut], n[kOut], k[kOut][kTaps];
 };
 
+// The 8 weights of a window as byte planes for v_dot4_u32_u8: word 3 * g + b
+// holds byte b of the weights of inputs 4g..4g+3.  A weight is below 2^23,
+// so three planes hold it and sum_j x_j k_j = d0 + (d1 << 8) + (d2 << 16),
+// d_b the byte-plane dot products, exactly.
+__host__ __device__ inline void pack_weights(const std::int32_t k[kWindow], std::uint32_t out[6]) {
+    for (std::uint32_t g = 0; g < 2; ++g)
+        for (std::uint32_t b = 0; b < 3; ++b) {
+            std::uint32_t w = 0;
+            for (std::uint32_t i = 0; i < 4; ++i)
+                w |= ((static_cast<std::uint32_t>(k[4 * g + i]) >> (8 * b)) & 0xFFu) << (8 * i);
+            out[3 * g + b] = w;
+        }
+}
+
+// Vertical pass weights as the kernel reads them: first input row, input
+// count, byte planes (6 words, padded to 8 for two 16-byte reads).
+struct Vertical {
+    std::int32_t lo[kOut], n[kOut];
+    std::uint32_t kb[kOut][8];
+};
+
 // The part of the tables the render kernel keeps in LDS.
 struct Staged {
-    Axis<kVTaps> v;          // 240 rows -> 84
+    Vertical v;              // 240 rows -> 84
     std::uint8_t gray[64];   // gray level of each palette colour
     std::uint8_t rgb[192];   // the renderer's RGB palette (64 x 3)
 };

@@ -32,7 +32,9 @@
 //     outputs as 8-byte runs (coalesced across the 32 threads of a row), and
 //     the band's gray levels feed the horizontal resample pass in LDS; the
 //     vertical pass runs once the intermediate rows an output row needs are
-//     complete.
+//     complete.  Both passes sum an 8-input window with 4-way byte dot
+//     products over the weights' byte planes (exact), and run beside the
+//     next band's phases, so a band costs two barriers.
 // Pattern tables (8 KB, shared by every console) are staged in LDS per
 // workgroup with the two planes of a tile row side by side, zeros for CHR RAM.
 #include <hip/hip_runtime.h>
@@ -63,7 +65,7 @@ constexpr std::uint32_t kNoSprite = 0xFFFFFFFFu;
 // The tables are staged in 16-byte words and a row of vertical weights is
 // read as two of them.
 static_assert(offsetof(render::Tables, s) % 16 == 0 && sizeof(render::Staged) % 16 == 0, "tables staged in 16-byte words");
-static_assert(offsetof(render::Staged, v.k) % 16 == 0 && render::kVTaps == 8, "vertical weights: two 16-byte reads per row");
+static_assert(offsetof(render::Staged, v.kb) % 16 == 0, "vertical weights: two 16-byte reads per row");
 
 // Scroll/ctrl pair one part of the frame is drawn with.
 struct View {
@@ -158,12 +160,13 @@ __device__ __forceinline__ uint2 bytes8(const std::uint8_t* row, std::uint32_t p
 }
 
 // Pillow's fixed-point sum of 8 consecutive 8-bit inputs (bytes of w) with
-// weights k (each in [0, 2^22], so 24-bit products are exact), rounded.
-__device__ __forceinline__ std::int32_t window8(const uint2 w, const std::int32_t k[8]) {
-    std::int32_t acc = 1 << (render::kPrecision - 1);
-    for (std::uint32_t j = 0; j < 4; ++j) acc += __mul24(static_cast<std::int32_t>((w.x >> (8 * j)) & 0xFF), k[j]);
-    for (std::uint32_t j = 0; j < 4; ++j) acc += __mul24(static_cast<std::int32_t>((w.y >> (8 * j)) & 0xFF), k[4 + j]);
-    return acc;
+// weights given as byte planes (pack_weights), rounded: three pairs of
+// 4-way byte dot products.
+__device__ __forceinline__ std::int32_t window8(const uint2 w, const std::uint32_t kb[6]) {
+    std::uint32_t d[3];
+    for (std::uint32_t b = 0; b < 3; ++b)
+        d[b] = __builtin_amdgcn_udot4(w.y, kb[3 + b], __builtin_amdgcn_udot4(w.x, kb[b], 0u, false), false);
+    return static_cast<std::int32_t>((1u << (render::kPrecision - 1)) + d[0] + (d[1] << 8) + (d[2] << 16));
 }
 
 __device__ __forceinline__ std::uint32_t clip8(std::int32_t acc) {
@@ -280,14 +283,16 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
     // read inside the row).
     const std::uint32_t h_rows = tid < 3 * render::kOut ? 1u : 0u;
     const std::uint32_t h_ox = tid % render::kOut, h_r0 = tid / render::kOut;
-    std::int32_t h_k[render::kWindow];
+    std::int32_t h_w[render::kWindow];
     const render::Axis<render::kHTaps>& ht = a.tables->h;
     const std::int32_t first = ht.lo[h_ox], taps = ht.n[h_ox];
     const std::uint32_t h_lo = first + render::kWindow > 256 ? 256 - render::kWindow : first;
     for (std::uint32_t j = 0; j < render::kWindow; ++j) {
         const std::int32_t k = static_cast<std::int32_t>(j + h_lo) - first;   // tap index of input h_lo + j
-        h_k[j] = (k >= 0 && k < taps) ? ht.k[h_ox][k] : 0;
+        h_w[j] = (k >= 0 && k < taps) ? ht.k[h_ox][k] : 0;
     }
+    std::uint32_t h_k[6];
+    render::pack_weights(h_w, h_k);
     // Band k is drawn in iteration k (background and sprites, then the merge)
     // while iteration k + 1 resamples it (horizontal pass beside band k + 1's
     // background and sprites, vertical pass beside its merge): two barriers a
@@ -405,9 +410,9 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
             std::uint8_t* out = a.gray + static_cast<std::size_t>(env) * render::kOut * render::kOut;
             for (std::uint32_t oy = next_oy + h_r0; h_rows != 0 && oy < end; oy += 3) {
                 const uint2 w = bytes8(mid[h_ox], tab.v.lo[oy] % kRing);
-                const int4* k = reinterpret_cast<const int4*>(tab.v.k[oy]);
-                const int4 k0 = k[0], k1 = k[1];
-                const std::int32_t kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                const uint4* k = reinterpret_cast<const uint4*>(tab.v.kb[oy]);
+                const uint4 k0 = k[0], k1 = k[1];
+                const std::uint32_t kv[6] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y};
                 out[oy * render::kOut + h_ox] = static_cast<std::uint8_t>(clip8(window8(w, kv)));
             }
             next_oy = end;
@@ -481,7 +486,13 @@ void axis(int in_size, std::int32_t* lo, std::int32_t* n, std::int32_t (*k)[kTap
 Tables make_tables() {
     Tables t{};
     axis<kHTaps>(256, t.h.lo, t.h.n, t.h.k);
-    axis<kVTaps>(240, t.s.v.lo, t.s.v.n, t.s.v.k);
+    Axis<kVTaps> v;
+    axis<kVTaps>(240, v.lo, v.n, v.k);
+    for (std::uint32_t oy = 0; oy < kOut; ++oy) {
+        t.s.v.lo[oy] = v.lo[oy];
+        t.s.v.n[oy] = v.n[oy];
+        pack_weights(v.k[oy], t.s.v.kb[oy]);
+    }
     // numpy's float luma of the RGB frame (an FMA chain over the channels),
     // truncated to uint8.
     for (std::uint32_t c = 0; c < 64; ++c) {
