@@ -146,6 +146,70 @@ def test_frames_of_random_ppu_states():
     _check(b, oracles, "random state")
 
 
+def _crafted_oam(rng: np.random.Generator, kind: int) -> np.ndarray:
+    """OAM (64 sprites) of one layout: 0 stacks of same-position sprites with
+    mixed priority/flip/palette, 1 sprites on the left and right screen edges
+    and the top/bottom rows, 2 a column of 8x16-style vertical neighbours, 3
+    uniform random."""
+    oam = rng.integers(0, 256, 256, dtype=np.uint8).reshape(64, 4)
+    if kind == 0:
+        for g in range(8):
+            y, x = rng.integers(0, 232), rng.integers(0, 256)
+            oam[8 * g:8 * g + 8, 0] = y + rng.integers(0, 3, 8)
+            oam[8 * g:8 * g + 8, 3] = x + rng.integers(0, 3, 8)
+    elif kind == 1:
+        oam[:, 3] = rng.choice(np.r_[0:9, 247:256], 64)
+        oam[:, 0] = rng.choice(np.r_[0:8, 224:240, 239:256], 64)
+    elif kind == 2:
+        x = rng.integers(0, 256)
+        oam[:, 3] = x + rng.integers(-4, 5, 64)
+        oam[:, 0] = np.arange(64) * 4 + rng.integers(0, 4, 64)
+    return oam.reshape(-1)
+
+
+def test_frames_of_crafted_sprite_layouts():
+    """Sprite layouts that stress the lowest-index-wins rule and the window
+    edges (stacks of overlapping sprites with mixed priority, flips and
+    palettes; sprites on the left and right edges with and without left-column
+    clipping; the top and bottom rows; 8x8 and 8x16), over every fine-x
+    scroll and y scrolls past 239, with palettes holding zero values (a
+    transparent background colour): the device renderer equals the oracle's
+    on every console."""
+    rom = _rom(5)
+    n = 256
+    say(f"[gpu] frames crafted sprite layouts: N={n}")
+    b = abi.Batch(rom, n, frameskip=1)
+    base = O.Oracle(rom)
+    for k in range(12):
+        base.step(int(masks_for(6, 1, k)[0]), 1)
+    st0 = base.save()
+    rng = np.random.default_rng(77)
+    states = []
+    for e in range(n):
+        st = st0.copy()
+        st[O.OFF["oam"]:O.OFF["oam"] + 256] = _crafted_oam(rng, e % 4)
+        pal = rng.integers(0, 64, 32, dtype=np.uint8)
+        pal[rng.integers(0, 32, 6)] = 0
+        st[O.OFF["palette"]:O.OFF["palette"] + 32] = pal
+        st[O.OFF["nametable"]:O.OFF["nametable"] + 2048] = rng.integers(0, 256, 2048, dtype=np.uint8)
+        st[O.OFF["ctrl"]] = (rng.integers(0, 256) & ~0x20) | (0x20 if e % 8 >= 4 else 0)
+        st[O.OFF["mask"]] = 0x18 | (rng.integers(0, 256) & 0x07) if e % 16 else rng.integers(0, 256)
+        st[O.OFF["scroll_x"]] = e % 8 + 8 * rng.integers(0, 32)
+        st[O.OFF["scroll_y"]] = rng.integers(0, 256)
+        states.append(st)
+    # One load per console (masked), then one render of the whole batch.
+    oracles = {}
+    for e, st in enumerate(states):
+        mask = np.zeros(n, dtype=np.uint8)
+        mask[e] = 1
+        b.load_state(st, mask)
+        con = O.Oracle(rom)
+        con.load(st)
+        con.seed_presentation()
+        oracles[e] = con
+    _check(b, oracles, "crafted sprites")
+
+
 @pytest.mark.parametrize("num_envs", [4096])
 def test_frames_full_size_sampled(num_envs):
     rom = _rom(11)
