@@ -66,6 +66,14 @@ constexpr std::uint32_t kNoSprite = 0xFFFFFFFFu;
 // read as two of them.
 static_assert(offsetof(render::Tables, s) % 16 == 0 && sizeof(render::Staged) % 16 == 0, "tables staged in 16-byte words");
 static_assert(offsetof(render::Staged, v.kb) % 16 == 0, "vertical weights: two 16-byte reads per row");
+// LDS of one workgroup, the sum of the kernel's shared arrays.  LDS is
+// allocated in 1,280-byte units: 32,000 bytes (25 units) lets 5 workgroups
+// share a compute unit's 160 KiB; one unit more leaves room for 4, and the
+// kernel runs about 14 % slower.
+constexpr std::size_t kLdsBytes = 2 * 4096 + present::kMaxBytes + 4 * kBand * 256 + 2 * kBand * kGrayStride +
+                                  render::kOut * kMidStride + sizeof(render::Staged) + 2 * 4 * sizeof(uint2) +
+                                  4 * sizeof(std::uint32_t) + kWaves * 64;
+static_assert(kLdsBytes <= 32000, "render kernel LDS above 25 allocation units: 4 workgroups per compute unit");
 
 // Scroll/ctrl pair one part of the frame is drawn with.
 struct View {
