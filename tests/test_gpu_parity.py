@@ -202,7 +202,8 @@ def test_largest_batch_sampled():
     """The largest batch, NESLE_MAX_ENVS = 262,144 consoles: 1,024 workgroups
     of 256 consoles, four to a compute unit in turn, and RAM/PRG-RAM offsets up
     to 2.7e9.  Sampled consoles at workgroup-round and range edges equal the
-    oracle (instruction counts and rewards every step, state at the end)."""
+    oracle (instruction counts and rewards every step, state and 84x84 gray
+    frame at the end)."""
     rom = _rom(2026)
     n = abi.MAX_ENVS
     rng = np.random.default_rng(11)
@@ -221,6 +222,12 @@ def test_largest_batch_sampled():
     for e, ref in zip(sample, ob.states()):
         got = b.save_state(e)
         assert np.array_equal(got, ref), f"env {e}: {first_diff(got, ref)}"
+    # One render of the whole batch (262,144 workgroups, gray offsets up to
+    # 1.8e9): the sampled consoles' 84x84 gray frames equal the oracle's.
+    b.render(abi.FRAME_GRAY84)
+    gray = b.host(abi.VIEW_GRAY84)
+    for e, con in zip(sample, ob.cons):
+        assert np.array_equal(gray[e], O.gray84(con.render(snapshot=True))), f"env {e}: gray84"
     b.close()
 
 
