@@ -280,6 +280,51 @@ def test_benchmark_workload_long_run_full_size_sampled():
     assert ends >= len(sample) + 16
 
 
+def test_benchmark_workload_soak_full_size_sampled():
+    """A soak of the benchmark workload: 65,536 consoles, 240 steps (960
+    frames, many episodes per console, each restarting from one of 8
+    snapshots), x-delta reward and auto-reset; 16 sampled consoles have the
+    oracle's rewards and dones at every step and its state every 40th step."""
+    rom = synthrom.make_rom(2026).rom
+    snaps = warm_snapshots(rom, [120, 233, 301, 415, 502, 611, 702, 777], seed=91)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 3 + 3 * i   # episodes of 24-192 frames from a snapshot
+    blobs = [bytes(s) for s in snaps]
+    n, steps = 65536, 240
+    rng = np.random.default_rng(92)
+    levels = rng.integers(0, 8, n).astype(np.uint8)
+    done_init = rng.integers(1, 25, n).astype(np.uint8)
+    sample = sorted({0, 63, 64, 16383, 32768, n - 1} | set(rng.integers(0, n, 10).tolist()))
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.01)
+    say(f"[gpu] benchmark workload soak: N={n} fs=4 steps={steps} sample={sample}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.01)
+    b.set_snapshots(blobs, levels)
+    b.poke_ram_envs(synthrom.DONE_BYTE, done_init)
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        c.load(snaps[levels[e]])
+        c.write(synthrom.DONE_BYTE, int(done_init[e]))
+    ends = 0
+    for k in range(steps):
+        m = masks_for(9191, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES)[sample], don, err_msg=f"step {k} dones")
+        for j in np.nonzero(don)[0]:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += int(don.sum())
+        if k % 40 == 39:
+            say(f"[gpu]   step {k}: {ends} sampled episode ends so far")
+            for e, ref in zip(sample, ob.states()):
+                got = b.save_state(e)
+                assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+    assert ends >= 5 * len(sample)
+
+
 def test_reset_envs_and_state_roundtrip():
     """Masked reset returns exactly the selected consoles to power-on; a saved
     state loaded into other consoles makes them identical; int64 device
