@@ -30,11 +30,15 @@
 //    status, open bus, write toggle, pads) are packed into VGPRs, so those
 //    reads take no LDS round trip; the other PPU registers live in a
 //    per-console LDS area.
-//  * Only the HBM operand load and the I/O register read branch inside the
-//    loop (PPUSTATUS and pad 1 reads by selects, the rest behind a branch);
-//    everything rare (I/O writes, JMP indirect, stack wrap, idle loops,
-//    illegal opcodes, PPU events, OAM DMA, code outside ROM) sits behind one
-//    wave-uniform test.
+//  * With RAM split between LDS and HBM, the next instruction is decoded one
+//    iteration ahead: its effective address is computed and its HBM operand
+//    load issued at the end of the current iteration, so the load has a
+//    whole iteration to arrive.  HBM operand loads and stores are branch-free
+//    (lanes without one read row 0 and write a spare row).
+//  * Only the I/O register read branches inside the loop (PPUSTATUS and pad 1
+//    reads by selects, the rest behind a branch); everything rare (I/O
+//    writes, JMP indirect, stack wrap, idle loops, illegal opcodes, PPU
+//    events, OAM DMA, code outside ROM) sits behind one wave-uniform test.
 //  * OAM DMA is done by the whole wave for one console at a time (4 bytes per
 //    lane) instead of a 256-iteration loop in one lane.
 //  * The CPU cycle counter is not updated per instruction: every cycle is 3
