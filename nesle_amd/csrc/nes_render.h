@@ -48,14 +48,14 @@ struct Vertical {
 // The part of the tables the render kernel keeps in LDS.
 struct Staged {
     Vertical v;              // 240 rows -> 84
-    std::uint8_t gray[64];   // gray level of each palette colour
-    std::uint8_t rgb[192];   // the renderer's RGB palette (64 x 3)
+    std::uint32_t rgb[64];   // the renderer's RGB palette: R | G << 8 | B << 16
 };
 
 // Everything the render kernel looks up, uploaded once per batch.
 struct Tables {
     Axis<kHTaps> h;          // 256 columns -> 84, read once per thread
     Staged s;
+    std::uint8_t gray[64];   // gray level of each palette colour, read once per console
 };
 
 // Host: the resize weights of Pillow's BILINEAR filter (libImaging/Resample.c

@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
                 p = value(16 + 4 * q + c);
             }
             v |= p << (8 * c);
-            g |= static_cast<std::uint32_t>(tab.gray[p]) << (8 * c);
+            g |= static_cast<std::uint32_t>(a.tables->gray[p]) << (8 * c);
         }
         if (tid < 4) {
             bgw[q] = make_uint2(v, g);
@@ -395,14 +395,14 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
             }
             const std::size_t pix = static_cast<std::size_t>(env) * 240 * 256 + y * 256 + x0;
             if (a.palette) *reinterpret_cast<uint2*>(a.palette + pix) = make_uint2(d[0], d[1]);
-            if (a.rgb) {
-                std::uint32_t w[6] = {0, 0, 0, 0, 0, 0};
-                for (std::uint32_t i = 0; i < 8; ++i) {
-                    const std::uint32_t c = byte_of(d, i);
-                    for (std::uint32_t ch = 0; ch < 3; ++ch) {
-                        const std::uint32_t b = 3 * i + ch;
-                        w[b >> 2] |= static_cast<std::uint32_t>(tab.rgb[3 * c + ch]) << (8 * (b & 3));
-                    }
+            if (a.rgb) {   // 8 pixels' RGB: one palette word per pixel, packed by 3 permutes per 4 pixels
+                std::uint32_t c[8], w[6];
+                for (std::uint32_t i = 0; i < 8; ++i) c[i] = tab.rgb[byte_of(d, i)];
+                for (std::uint32_t h = 0; h < 2; ++h) {
+                    const std::uint32_t* q = c + 4 * h;
+                    w[3 * h] = perm(q[1], q[0], 0x04020100u);       // R0 G0 B0 R1
+                    w[3 * h + 1] = perm(q[2], q[1], 0x05040201u);   // G1 B1 R2 G2
+                    w[3 * h + 2] = perm(q[3], q[2], 0x06050402u);   // B2 R3 G3 B3
                 }
                 uint2* o = reinterpret_cast<uint2*>(a.rgb + pix * 3);
                 o[0] = make_uint2(w[0], w[1]);
@@ -505,9 +505,10 @@ Tables make_tables() {
     // truncated to uint8.
     for (std::uint32_t c = 0; c < 64; ++c) {
         const double r = kNesRgbHost[3 * c], g = kNesRgbHost[3 * c + 1], b = kNesRgbHost[3 * c + 2];
-        t.s.gray[c] = static_cast<std::uint8_t>(static_cast<int>(std::fma(b, 0.114, std::fma(g, 0.587, r * 0.299))));
+        t.gray[c] = static_cast<std::uint8_t>(static_cast<int>(std::fma(b, 0.114, std::fma(g, 0.587, r * 0.299))));
     }
-    for (std::uint32_t i = 0; i < 192; ++i) t.s.rgb[i] = kNesRgbHost[i];
+    for (std::uint32_t c = 0; c < 64; ++c)
+        t.s.rgb[c] = kNesRgbHost[3 * c] | (kNesRgbHost[3 * c + 1] << 8) | (static_cast<std::uint32_t>(kNesRgbHost[3 * c + 2]) << 16);
     return t;
 }
 
