@@ -110,6 +110,32 @@ def test_full_size_sampled_envs(num_envs, steps):
     assert (b.host(abi.VIEW_BUDGET_HITS) == 0).all()
 
 
+@pytest.mark.parametrize("num_envs", [1, 100, 12345, 50001])
+def test_ragged_batch_sizes_sampled(num_envs):
+    """Batch sizes that fill no whole wave or workgroup: 1 and 100 consoles
+    (all RAM in LDS), 12,345 (16 consoles a wave) and 50,001 (64 a wave, the
+    last wave holding 17).  Sampled consoles, the last one always among them,
+    equal the oracle over 3 steps (instruction counts and rewards every step,
+    state at the end)."""
+    rom = _rom(13)
+    rng = np.random.default_rng(num_envs)
+    sample = sorted({0, num_envs - 1, *(rng.integers(0, num_envs, 6).tolist() if num_envs > 1 else [])})
+    say(f"[gpu] ragged size: N={num_envs} fs=4 sample={sample}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    ob = OracleBatch(rom, sample)
+    for k in range(3):
+        m = masks_for(4321, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, _ = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_INSTRUCTIONS)[sample], ins, err_msg=f"step {k}")
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k}")
+    for e, ref in zip(sample, ob.states()):
+        got = b.save_state(e)
+        assert np.array_equal(got, ref), f"env {e}: {first_diff(got, ref)}"
+    assert (b.host(abi.VIEW_FRAMES) == 4).all()
+
+
 def test_snapshot_autoreset_xdelta_reward():
     """Config 3 in miniature: 8 snapshots captured after seeded warm-up frames,
     done byte patched so episodes end within the run, x-delta reward with time
