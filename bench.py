@@ -190,22 +190,29 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
     # Dones of the timed steps, summed on the device (one elementwise add per step).
     dones = torch.from_dlpack(batch.last_done_device())
     done_count = torch.zeros(num_envs, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
-    for k in range(warmup):
-        batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
-        if gray84:
-            batch.render_frames_device(rgb=False, palette=False, gray84=True)
-    torch.cuda.synchronize()
-    batch.set_timing(True)
-    t0 = time.perf_counter()
-    for k in range(warmup, warmup + steps):
+
+    def one_step(k: int) -> None:
         batch.step_device(table[k], auto_reset=auto_reset, synchronize=False)
         done_count.add_(dones)
         if gray84:
             batch.render_frames_device(rgb=False, palette=False, gray84=True)
+
+    # The warm-up runs exactly the timed loop's body (every launch of it has
+    # run once before timing starts), with the event timing on, whose event
+    # objects are created by set_timing.
+    batch.set_timing(True)
+    for k in range(warmup):
+        one_step(k)
+    torch.cuda.synchronize()
+    done_count.zero_()
+    batch.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(warmup, warmup + steps):
+        one_step(k)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    kernel_ms, launches = batch.kernel_timing()
+    kernel_ms, reset_ms, launches = batch.kernel_timing_split()
     batch.set_timing(False)
     done_total = int(done_count.sum().item())
     # Exact emulated instruction count per env-step from one stats step.
@@ -218,6 +225,8 @@ def run_gpu(core, rom: bytes, num_envs: int, steps: int, warmup: int, snapshots:
         "env_steps_per_s": num_envs * steps / elapsed,
         "ms_per_step": 1000.0 * elapsed / steps,
         "kernel_ms_per_launch": kernel_ms / max(launches, 1),
+        "restore_ms_per_launch": reset_ms / max(launches, 1),
+        "kernels_ms_per_step": (kernel_ms + reset_ms) / max(launches, 1),
         "kernel_launches": launches,
         "instructions_per_env_step": float(instr.mean()),
         "dones_in_timed_window": done_total,
@@ -262,7 +271,8 @@ def run_reset_burst(core, rom: bytes, snapshots: list[bytes], levels: np.ndarray
             b.set_timing(True)
             b.step_device(table[k], auto_reset=ar, synchronize=False)
             torch.cuda.synchronize()
-            ms.append(b.kernel_timing()[0])
+            step_ms, reset_ms, _ = b.kernel_timing_split()
+            ms.append(step_ms + reset_ms)
             b.set_timing(False)
         dones = torch.from_dlpack(pair[1].last_done_device()).clone()
         pair[1].reset_envs_device(dones)
@@ -387,18 +397,89 @@ def cpu_baseline(rom: bytes, snaps: list[bytes], levels: np.ndarray, done_init: 
         "per_core": value / threads,
         "instructions_per_env_step": instr / (envs * steps),
         "cpu_model": _cpu_model(),
+        "build": "g++ 11 -O3 -march=x86-64-v3 (oracle/Makefile: built beside the GPU code and shipped with it, "
+                 "so the ISA level is fixed rather than -march=native of the machine that runs it)",
         **share,
     }
 
 
 def _cpu_model() -> str:
+    """Model name, family/model/stepping and clock of the host CPU from
+    /proc/cpuinfo (some hosts report only the vendor in the model name)."""
     try:
+        info = {}
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, value = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model", "stepping", "cpu MHz") and key not in info:
+                info[key] = value.strip()
+        if info:
+            return (f"{info.get('model name', '?')} (family {info.get('cpu family', '?')}, model "
+                    f"{info.get('model', '?')}, stepping {info.get('stepping', '?')}, {info.get('cpu MHz', '?')} MHz)")
     except OSError:
         pass
     return "unknown"
+
+
+def run_census(rom: bytes, snaps: list[bytes], levels: np.ndarray | None, done_init: np.ndarray | None,
+               num_envs: int, steps: int, warmup: int) -> dict:
+    """The step kernel's census (stats mode 3) over ``steps`` steps of a
+    workload, after ``warmup`` ordinary steps: per wave-iteration, how often
+    a wave takes the rare path and why, the I/O read side path, OAM DMA and
+    the presentation capture, active lanes and distinct microcode entries,
+    and the shader cycles in the loop, the rare path and the I/O read path.
+    With ``snaps`` the 65,536-console workload's snapshot levels, staggered
+    done bytes and auto-reset; without, the 4,096-console one (no resets).
+    Also times the same steps without the census (HIP events) to relate
+    cycles to time."""
+    from nesle_amd import abi
+
+    b = abi.Batch(rom, num_envs, 4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=TIME_PENALTY)
+    auto_reset = snaps is not None
+    if auto_reset:
+        b.set_snapshots(snaps, levels)
+        b.poke_ram_envs(synthrom.DONE_BYTE, done_init)
+    for k in range(warmup):
+        b.set_actions(synthrom.action_masks(ACTION_SEED, num_envs, k))
+        b.step(auto_reset=auto_reset)
+    totals: dict[str, int] = {}
+    ms_plain = []
+    for k in range(warmup, warmup + steps):
+        b.set_actions(synthrom.action_masks(ACTION_SEED, num_envs, k))
+        b.set_timing(True)
+        b.step(auto_reset=auto_reset, stats_mode=3)
+        b.synchronize()
+        census_ms = b.timing()[0]
+        for name, value in b.census().items():
+            totals[name] = totals.get(name, 0) + value
+        totals["census_kernel_us"] = totals.get("census_kernel_us", 0) + int(1000 * census_ms)
+        instr = b.host(abi.VIEW_INSTRUCTIONS).astype(np.float64)
+        totals["instructions"] = totals.get("instructions", 0) + int(instr.sum())
+    # The same number of ordinary steps, timed, for the kernel's plain speed.
+    for k in range(warmup + steps, warmup + 2 * steps):
+        b.set_actions(synthrom.action_masks(ACTION_SEED, num_envs, k))
+        b.set_timing(True)
+        b.step(auto_reset=auto_reset)
+        b.synchronize()
+        ms_plain.append(b.timing()[0])
+    b.close()
+    it = max(totals["iterations"], 1)
+    per_it = {k: totals[k] / it for k in totals if k not in ("waves", "iterations", "census_kernel_us",
+                                                             "instructions")}
+    waves = max(totals["waves"], 1)
+    plain_ms = float(np.mean(ms_plain))
+    return {
+        "num_envs": num_envs, "steps": steps, "warmup": warmup, "totals": totals,
+        "per_wave_iteration": per_it,
+        "wave_iterations_per_wave_per_step": totals["iterations"] / waves,
+        "cycles_per_wave_iteration": totals["cycles_loop"] / it,
+        "rare_cycles_per_rare_iteration": totals["cycles_rare"] / max(totals["rare"], 1),
+        "io_read_cycles_per_io_iteration": totals["cycles_io_read"] / max(totals["io_read"], 1),
+        "census_kernel_ms": totals["census_kernel_us"] / 1000.0 / steps,
+        "plain_kernel_ms": plain_ms,
+        "instructions_per_env_step": totals["instructions"] / (num_envs * steps),
+    }
 
 
 def copy_calibration(mib: int) -> int:
@@ -436,6 +517,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (scales rocprof FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--census", type=int, default=0, metavar="STEPS",
+                    help="only print the step kernel's census (stats mode 3) over STEPS steps of the 65,536- and "
+                         "4,096-console workloads")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
@@ -459,9 +543,16 @@ def main() -> int:
     levels = rng.integers(0, NUM_LEVELS, args.envs).astype(np.uint8)
     done_init = staggered_done(levels, done_vals)
 
+    if args.census:
+        out = {"census": [run_census(rom, snaps, levels, done_init, args.envs, args.census, args.warmup),
+                          run_census(rom, None, None, None, args.small_envs, args.census, max(5, args.warmup // 4))]}
+        print(json.dumps(out))
+        return 0
+
     log(f"timing {args.envs} envs x {args.steps} steps (warmup {args.warmup})")
     big = run_gpu(core, rom, args.envs, args.steps, args.warmup, snaps, levels, done_init=done_init)
-    log(f"  {big['env_steps_per_s']:.0f} env-steps/s, kernel {big['kernel_ms_per_launch']:.2f} ms/launch, "
+    log(f"  {big['env_steps_per_s']:.0f} env-steps/s, {big['ms_per_step']:.2f} ms/step: step kernel "
+        f"{big['kernel_ms_per_launch']:.2f} ms + restore {big['restore_ms_per_launch']:.3f} ms, "
         f"{big['dones_in_timed_window']} auto-resets while timed")
     burst = None
     if args.burst:
@@ -528,6 +619,8 @@ def main() -> int:
                       "this run); peak = 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz; traffic = HBM bytes per launch "
                       "(FETCH_SIZE x2.000 + WRITE_SIZE x1.000, same summary)",
             "kernel_ms_per_launch": big["kernel_ms_per_launch"],
+            "restore_ms_per_launch": big["restore_ms_per_launch"],
+            "window_over_kernels": big["ms_per_step"] / big["kernels_ms_per_step"] - 1.0,
             "emulated_instr_per_s": instr_rate,
             "instructions_per_env_step": big["instructions_per_env_step"],
             "valu_busy_frac": profile_figure("valu_busy", args.envs),

@@ -55,7 +55,8 @@ enum {
     NESLE_VIEW_FRAME_RGB = 10,   /* uint8  [num_envs][240][256][3] (after nesle_render) */
     NESLE_VIEW_FRAME_PALETTE = 11, /* uint8 [num_envs][240][256] palette values 0-63 */
     NESLE_VIEW_GRAY84 = 12,      /* uint8  [num_envs][84][84] gray observation */
-    NESLE_VIEW_COUNT = 13
+    NESLE_VIEW_CENSUS = 13,      /* uint64 [32] step-kernel census (after stats mode 3 steps) */
+    NESLE_VIEW_COUNT = 14
 };
 
 /* nesle_render outputs (bit mask). */
@@ -146,7 +147,11 @@ int nesle_set_actions(nesle_batch* b, const void* actions, int dtype, int on_dev
 
 /* Run one env-step on every console (frameskip frames, reward/done, optional
  * fused auto-reset of done consoles), then refresh the RAM view.
- * stats_mode: 0 none, 1 per-console counters, 2 also opcode/PC histograms.
+ * stats_mode: 0 none, 1 per-console counters, 2 also opcode/PC histograms,
+ * 3 per-console counters and the step kernel's census of the launch (how many
+ * wave-iterations took each side path and the rare path, by cause, and the
+ * shader cycles spent there; indices in nesle_amd/csrc/nes_layout.h,
+ * namespace census; no reference counterpart).
  * Replaces launch_console_step_kernel (kernels.cu:145-158) and the
  * step_device/step_stats/step_profile sequences (cuda_module.cu:594-818). */
 int nesle_step(nesle_batch* b, int auto_reset, int stats_mode);
@@ -205,14 +210,17 @@ int nesle_poke_ram_envs(nesle_batch* b, uint32_t address, const uint8_t* values,
 int nesle_synchronize(nesle_batch* b);
 int nesle_set_stream(nesle_batch* b, void* hip_stream);
 
-/* Step-kernel timing with HIP events recorded on the batch's stream around
- * every step-kernel launch while enabled (enable resets the totals).
- * nesle_get_timing synchronises and returns the summed kernel milliseconds
- * and the number of timed launches.  No reference counterpart: the
- * reference measures kernels only from its benchmark tools
- * (cpp/tools/benchmark_cuda_kernels.cu:74-198). */
+/* Step timing with HIP events recorded on the batch's stream while enabled
+ * (enable resets the totals): before every step-kernel launch, between it
+ * and the auto-reset's restore kernel, and after that.  nesle_get_timing
+ * synchronises and returns the summed step-kernel milliseconds and the
+ * number of timed steps; nesle_get_timing_split also returns the restore
+ * kernel's milliseconds (0 for steps without auto-reset).  Any out pointer
+ * may be null.  No reference counterpart: the reference measures kernels
+ * only from its benchmark tools (cpp/tools/benchmark_cuda_kernels.cu:74-198). */
 int nesle_set_timing(nesle_batch* b, int enable);
 int nesle_get_timing(nesle_batch* b, double* total_ms, uint64_t* launches);
+int nesle_get_timing_split(nesle_batch* b, double* step_ms, double* reset_ms, uint64_t* launches);
 
 uint32_t nesle_num_envs(const nesle_batch* b);
 uint32_t nesle_frameskip(const nesle_batch* b);

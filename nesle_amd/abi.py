@@ -26,6 +26,12 @@ REWARD_SMB, REWARD_XDELTA = 0, 1
 VIEW_RAM, VIEW_REWARDS, VIEW_DONES, VIEW_ACTIONS = 0, 1, 2, 3
 VIEW_INSTRUCTIONS, VIEW_FRAMES, VIEW_BUDGET_HITS, VIEW_OPCODES, VIEW_PCS, VIEW_OAM = 4, 5, 6, 7, 8, 9
 VIEW_FRAME_RGB, VIEW_FRAME_PALETTE, VIEW_GRAY84 = 10, 11, 12
+VIEW_CENSUS = 13
+# Step-kernel census slots (nesle_amd/csrc/nes_layout.h, namespace census).
+CENSUS_FIELDS = ("waves", "iterations", "rare", "rare_io_write", "rare_side", "rare_idle", "rare_illegal",
+                 "rare_timing", "rare_budget", "rare_outside", "rare_only_io_write", "dma", "present", "io_read",
+                 "io_read_slow", "active_lanes", "distinct_entries", "cycles_loop", "cycles_rare", "cycles_io_read",
+                 "lanes_io_write", "lanes_timing", "lanes_io_read", "lanes_io_read_slow", "exits")
 FRAME_RGB, FRAME_PALETTE, FRAME_GRAY84 = 1, 2, 4
 DTYPE_U8, DTYPE_I64, DTYPE_F32, DTYPE_U32, DTYPE_U64 = 0, 1, 2, 3, 4
 STATE_BYTES = 22896
@@ -132,6 +138,8 @@ def lib():
         "nesle_device_id": (ctypes.c_int32, [vp]),
         "nesle_set_timing": (ctypes.c_int, [vp, ctypes.c_int]),
         "nesle_get_timing": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint64)]),
+        "nesle_get_timing_split": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                                  ctypes.POINTER(ctypes.c_uint64)]),
         "nesle_parse_ines": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(RomInfo)]),
         "nesle_parse_fcs": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, _U8P]),
         "nesle_last_error": (ctypes.c_char_p, []),
@@ -228,6 +236,11 @@ class Batch:
     def step(self, auto_reset: bool = False, stats_mode: int = 0) -> None:
         _check(lib().nesle_step(self.h, int(auto_reset), stats_mode))
 
+    def census(self) -> dict:
+        """The step kernel's census of the last stats-mode-3 step, by name."""
+        raw = self.host(VIEW_CENSUS)
+        return {name: int(raw[i]) for i, name in enumerate(CENSUS_FIELDS)}
+
     def reset(self) -> None:
         _check(lib().nesle_reset(self.h))
 
@@ -247,7 +260,7 @@ class Batch:
               VIEW_BUDGET_HITS: (np.uint32, (self.n,)), VIEW_OPCODES: (np.uint64, (256,)),
               VIEW_PCS: (np.uint64, (65536,)), VIEW_OAM: (np.uint8, (self.n, 256)),
               VIEW_FRAME_RGB: (np.uint8, (self.n, 240, 256, 3)), VIEW_FRAME_PALETTE: (np.uint8, (self.n, 240, 256)),
-              VIEW_GRAY84: (np.uint8, (self.n, 84, 84))}[kind]
+              VIEW_GRAY84: (np.uint8, (self.n, 84, 84)), VIEW_CENSUS: (np.uint64, (32,))}[kind]
         out = np.empty(dt[1], dtype=dt[0])
         _check(lib().nesle_copy_to_host(self.h, kind, out.ctypes.data, out.nbytes))
         return out
@@ -302,6 +315,12 @@ class Batch:
         n = ctypes.c_uint64()
         _check(lib().nesle_get_timing(self.h, ctypes.byref(ms), ctypes.byref(n)))
         return ms.value, n.value
+
+    def timing_split(self) -> tuple[float, float, int]:
+        """(step-kernel ms, auto-reset restore-kernel ms, timed steps) since enabling."""
+        ms, reset_ms, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_uint64()
+        _check(lib().nesle_get_timing_split(self.h, ctypes.byref(ms), ctypes.byref(reset_ms), ctypes.byref(n)))
+        return ms.value, reset_ms.value, n.value
 
     @property
     def num_levels(self) -> int:

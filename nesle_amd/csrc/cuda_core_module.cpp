@@ -425,6 +425,12 @@ public:
         check(nesle_get_timing(h_, &ms, &n));
         return py::make_tuple(ms, n);
     }
+    py::tuple kernel_timing_split() const {
+        double ms = 0.0, reset_ms = 0.0;
+        std::uint64_t n = 0;
+        check(nesle_get_timing_split(h_, &ms, &reset_ms, &n));
+        return py::make_tuple(ms, reset_ms, n);
+    }
     void set_stream(std::uintptr_t stream) { check(nesle_set_stream(h_, reinterpret_cast<void*>(stream))); }
 
     std::uint32_t num_envs() const { return n_; }
@@ -612,6 +618,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("synchronize", &CudaBatch::synchronize)
         .def("set_timing", &CudaBatch::set_timing, py::arg("enable"))
         .def("kernel_timing", &CudaBatch::kernel_timing)
+        .def("kernel_timing_split", &CudaBatch::kernel_timing_split)
         .def("set_stream", &CudaBatch::set_stream, py::arg("stream"))
         .def_property_readonly("name", [](const CudaBatch&) { return std::string("cuda-console"); })
         .def_property_readonly("has_snapshot", &CudaBatch::has_snapshot)

@@ -68,12 +68,12 @@ struct Rom {
 };
 
 Rom parse_ines(const std::uint8_t* b, std::size_t n) {
-    if (b == nullptr || n < 16) throw InvalidArgument("iNES data is shorter than the 16-byte header");
+    if (b == nullptr || n < 16) throw InvalidArgument("iNES image shorter than its 16-byte header");
     if (b[0] != 'N' || b[1] != 'E' || b[2] != 'S' || b[3] != 0x1A)
-        throw InvalidArgument("iNES header magic must be NES<EOF>");
+        throw InvalidArgument("iNES image: bad magic, the first four bytes are not N E S 0x1A");
     Rom r;
     const bool nes2 = (b[7] & 0x0C) == 0x08;
-    if (nes2 && b[9] != 0) throw InvalidArgument("NES 2.0 extended PRG/CHR ROM sizes are not supported yet");
+    if (nes2 && b[9] != 0) throw InvalidArgument("NES 2.0 image with extended (exponent form) PRG/CHR sizes: not handled");
     r.info.is_nes2 = nes2;
     r.info.mapper = (b[6] >> 4) | (b[7] & 0xF0);
     if (nes2) {
@@ -87,7 +87,7 @@ Rom parse_ines(const std::uint8_t* b, std::size_t n) {
     r.info.chr_rom_size = b[5] * 8192u;
     std::size_t off = 16 + (r.info.has_trainer ? 512 : 0);
     if (n < off + r.info.prg_rom_size + r.info.chr_rom_size)
-        throw InvalidArgument("iNES data is truncated for declared PRG/CHR sizes");
+        throw InvalidArgument("iNES image truncated: fewer bytes than its header declares for trainer, PRG and CHR");
     r.prg.assign(b + off, b + off + r.info.prg_rom_size);
     off += r.info.prg_rom_size;
     r.chr.assign(b + off, b + off + r.info.chr_rom_size);
@@ -102,9 +102,9 @@ std::uint32_t rd_le32(const std::uint8_t* p) {
 }
 
 void fcs_to_blob(const std::uint8_t* d, std::size_t n, std::uint8_t* o) {
-    if (n < 16) throw std::runtime_error("FCS: header too short");
+    if (n < 16) throw std::runtime_error("FCEUX state: fewer than 16 bytes, no room for the file header");
     if (d[0] != 'F' || d[1] != 'C' || d[2] != 'S' || d[3] != 0xFF)
-        throw std::runtime_error("FCS: bad magic (expected 'FCS\\xff')");
+        throw std::runtime_error("FCEUX state: the file does not start with the signature F C S 0xFF");
     std::memset(o, 0, blob::kBytes);
     std::memcpy(o, "NST1", 4);
     o[blob::kSp] = 0xFD;
@@ -119,17 +119,17 @@ void fcs_to_blob(const std::uint8_t* d, std::size_t n, std::uint8_t* o) {
             const std::string name(reinterpret_cast<const char*>(pay + off), nl);
             const std::uint32_t size = rd_le32(pay + off + 4);
             off += 8;
-            if (off + size > len) throw std::runtime_error("FCS: sub-chunk \"" + name + "\" extends past parent payload");
+            if (off + size > len) throw std::runtime_error("FCEUX state: field " + name + " of a section runs beyond that section");
             const std::uint8_t* v = pay + off;
             auto fixed = [&](std::uint32_t dst, std::uint32_t want, const char* label) {
                 if (size != want)
-                    throw std::runtime_error(std::string("FCS: ") + label + " expected " + std::to_string(want) +
-                                             " bytes, got " + std::to_string(size));
+                    throw std::runtime_error(std::string("FCEUX state: field ") + label + " holds " + std::to_string(size) +
+                                             " bytes where " + std::to_string(want) + " belong");
                 std::memcpy(o + dst, v, want);
             };
             if (tag == 1) {
                 if (name == "PC") {
-                    if (size != 2) throw std::runtime_error("FCS: CPU.PC must be 2 bytes");
+                    if (size != 2) throw std::runtime_error("FCEUX state: field CPU.PC holds other than 2 bytes");
                     o[blob::kPc] = v[0];
                     o[blob::kPc + 1] = v[1];
                 } else if (size == 1 && (name == "A" || name == "X" || name == "Y" || name == "S" || name == "P")) {
@@ -147,7 +147,7 @@ void fcs_to_blob(const std::uint8_t* d, std::size_t n, std::uint8_t* o) {
                 } else if (name == "SPRA") {
                     fixed(blob::kOam, nesle::kOamBytes, "PPU.SPRA");
                 } else if (name == "PPUR") {
-                    if (size < 3) throw std::runtime_error("FCS: PPU.PPUR too short");
+                    if (size < 3) throw std::runtime_error("FCEUX state: field PPU.PPUR holds fewer than 3 bytes");
                     o[blob::kCtrl] = v[0];
                     o[blob::kMask] = v[1];
                     o[blob::kStatus] = v[2];
@@ -173,18 +173,18 @@ void fcs_to_blob(const std::uint8_t* d, std::size_t n, std::uint8_t* o) {
             }
             off += size;
         }
-        if (off != len) throw std::runtime_error("FCS: trailing bytes in sub-chunk stream");
+        if (off != len) throw std::runtime_error("FCEUX state: a section ends with a partial field header");
     };
     std::size_t off = 16;
     while (off + 5 <= n) {
         const int tag = d[off];
         const std::uint32_t size = rd_le32(d + off + 1);
         off += 5;
-        if (off + size > n) throw std::runtime_error("FCS: top-level chunk extends past file");
+        if (off + size > n) throw std::runtime_error("FCEUX state: a section runs beyond the end of the file");
         if (tag == 1 || tag == 3 || tag == 16) walk(d + off, size, tag);
         off += size;
     }
-    if (off != n) throw std::runtime_error("FCS: trailing bytes after last top-level chunk");
+    if (off != n) throw std::runtime_error("FCEUX state: the file ends with a partial section header");
 }
 
 // A snapshot blob in either format, as a canonical blob.
@@ -227,18 +227,25 @@ struct nesle_batch {
     std::uint8_t* d_frame_palette = nullptr;
     std::uint8_t* d_gray84 = nullptr;
     void* d_render_tables = nullptr;   // render::Tables
-    // Step-kernel timing: event pairs are recorded per launch and folded into
-    // the totals once the pair has completed.
+    // Step timing: three events per step (before the step kernel, between it
+    // and the auto-reset's restore kernel, after that), folded into the
+    // totals once the last has completed.
+    struct Marks { hipEvent_t start, stepped, reset; };
     bool timing = false;
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> events;  // recorded, not yet folded
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> spare;
-    double timed_ms = 0.0;
+    std::vector<Marks> events;  // recorded, not yet folded
+    std::vector<Marks> spare;
+    double timed_ms = 0.0;        // step kernel
+    double timed_reset_ms = 0.0;  // restore kernel of the auto-reset
     std::uint64_t timed_launches = 0;
 
     ~nesle_batch() {
         if (device >= 0) (void)hipSetDevice(device);
-        for (auto& e : events) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
-        for (auto& e : spare) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+        for (auto* list : {&events, &spare})
+            for (auto& e : *list) {
+                (void)hipEventDestroy(e.start);
+                (void)hipEventDestroy(e.stepped);
+                (void)hipEventDestroy(e.reset);
+            }
         (void)hipFree(arena);
         (void)hipFree(d_bank);
         (void)hipFree(stats_arena);
@@ -306,13 +313,15 @@ struct nesle_batch {
         if (stats_arena != nullptr) return;
         const std::size_t n = cfg.num_envs;
         const std::size_t a = align_up(8 * n, 256), b = align_up(4 * n, 256), c = align_up(4 * n, 256);
-        hip_check(hipMalloc(&stats_arena, a + b + c + 8 * 256 + 8 * 65536), "hipMalloc stats");
+        hip_check(hipMalloc(&stats_arena, a + b + c + 8 * 256 + 8 * 65536 + 8 * nesle::census::kCount),
+                  "hipMalloc stats");
         auto* base = static_cast<std::uint8_t*>(stats_arena);
         ds.stat_instructions = reinterpret_cast<std::uint64_t*>(base);
         ds.stat_frames = reinterpret_cast<std::uint32_t*>(base + a);
         ds.stat_budget_hits = reinterpret_cast<std::uint32_t*>(base + a + b);
         ds.prof_opcodes = reinterpret_cast<unsigned long long*>(base + a + b + c);
         ds.prof_pcs = ds.prof_opcodes + 256;
+        ds.census = ds.prof_pcs + 65536;
     }
 
     void refresh_obs() { hip_check(nesle::launch_ram_obs(ds, d_obs, stream), "ram_obs_kernel"); }
@@ -340,27 +349,32 @@ struct nesle_batch {
         host_to_device(d_render_tables, &t, sizeof(t), "upload render tables");
     }
 
-    std::pair<hipEvent_t, hipEvent_t> take_events() {
-        if (!spare.empty()) {
-            auto e = spare.back();
-            spare.pop_back();
-            return e;
-        }
-        std::pair<hipEvent_t, hipEvent_t> e{};
-        hip_check(hipEventCreate(&e.first), "hipEventCreate");
-        hip_check(hipEventCreate(&e.second), "hipEventCreate");
+    static Marks new_marks() {
+        Marks e{};
+        hip_check(hipEventCreate(&e.start), "hipEventCreate");
+        hip_check(hipEventCreate(&e.stepped), "hipEventCreate");
+        hip_check(hipEventCreate(&e.reset), "hipEventCreate");
         return e;
     }
 
-    // Fold completed event pairs into the totals (all of them when `wait`).
+    Marks take_events() {
+        if (spare.empty()) return new_marks();
+        const Marks e = spare.back();
+        spare.pop_back();
+        return e;
+    }
+
+    // Fold completed event triples into the totals (all of them when `wait`).
     void fold_events(bool wait) {
         std::size_t done = 0;
         for (auto& e : events) {
-            if (!wait && hipEventQuery(e.second) != hipSuccess) break;
-            hip_check(hipEventSynchronize(e.second), "hipEventSynchronize");
-            float ms = 0.0f;
-            hip_check(hipEventElapsedTime(&ms, e.first, e.second), "hipEventElapsedTime");
-            timed_ms += ms;
+            if (!wait && hipEventQuery(e.reset) != hipSuccess) break;
+            hip_check(hipEventSynchronize(e.reset), "hipEventSynchronize");
+            float step_ms = 0.0f, reset_ms = 0.0f;
+            hip_check(hipEventElapsedTime(&step_ms, e.start, e.stepped), "hipEventElapsedTime");
+            hip_check(hipEventElapsedTime(&reset_ms, e.stepped, e.reset), "hipEventElapsedTime");
+            timed_ms += step_ms;
+            timed_reset_ms += reset_ms;
             ++timed_launches;
             spare.push_back(e);
             ++done;
@@ -372,7 +386,7 @@ struct nesle_batch {
         if (want <= bank_capacity) return;
         std::uint32_t cap = std::max<std::uint32_t>(want, bank_capacity * 2);
         cap = std::min<std::uint32_t>(std::max<std::uint32_t>(cap, 8), 255);
-        if (want > cap) throw InvalidArgument("at most 255 snapshot levels supported per batch");
+        if (want > cap) throw InvalidArgument("a batch holds at most 255 snapshot levels");
         std::uint8_t* nb = nullptr;
         hip_check(hipMalloc(&nb, static_cast<std::size_t>(cap) * blob::kBytes), "hipMalloc snapshot bank");
         if (d_bank != nullptr && num_levels != 0) {
@@ -440,7 +454,7 @@ int nesle_create(const nesle_config* cfg, const std::uint8_t* ines, std::size_t 
         if (b->cfg.max_instructions_per_frame == 0) b->cfg.max_instructions_per_frame = 200000;
         b->rom = parse_ines(ines, ines_len);
         if (b->rom.info.mapper != 0 || (b->rom.prg.size() != 16384 && b->rom.prg.size() != 32768))
-            throw InvalidArgument("HIP console mode currently supports mapper 0/NROM ROMs");
+            throw InvalidArgument("only mapper 0 (NROM) cartridges run on this console");
         int dev = cfg->device;
         if (dev < 0) hip_check(hipGetDevice(&dev), "hipGetDevice");
         b->device = dev;
@@ -475,8 +489,8 @@ int nesle_set_snapshots(nesle_batch* b, const std::uint8_t* const* blobs, const 
                         const std::uint8_t* env_to_level) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
-        if (count == 0) throw InvalidArgument("snapshot_bytes_list must contain at least one snapshot");
-        if (count > 255) throw InvalidArgument("at most 255 snapshot levels supported per CudaBatch");
+        if (count == 0) throw InvalidArgument("the snapshot list is empty: give at least one snapshot");
+        if (count > 255) throw InvalidArgument("a batch holds at most 255 snapshot levels");
         std::vector<std::uint8_t> host(static_cast<std::size_t>(count) * blob::kBytes);
         for (std::uint32_t i = 0; i < count; ++i) {
             if (blobs[i] == nullptr) throw InvalidArgument("null snapshot");
@@ -573,7 +587,7 @@ int nesle_set_actions(nesle_batch* b, const void* actions, int dtype, int on_dev
 int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
-        if (stats_mode < 0 || stats_mode > 2) throw InvalidArgument("stats_mode must be 0, 1 or 2");
+        if (stats_mode < 0 || stats_mode > 3) throw InvalidArgument("stats_mode must be 0, 1, 2 or 3");
         b->activate();
         if (stats_mode != 0) {
             b->ensure_stats();
@@ -581,6 +595,8 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
                 // Opcode and PC histograms are contiguous.
                 hip_check(nesle::launch_zero_u64(b->ds.prof_opcodes, 256 + 65536, b->stream), "clear profile");
             }
+            if (stats_mode == 3)
+                hip_check(nesle::launch_zero_u64(b->ds.census, nesle::census::kCount, b->stream), "clear census");
         }
         DeviceState s = b->ds;
         if (stats_mode == 0) {
@@ -592,17 +608,22 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
             s.prof_opcodes = nullptr;
             s.prof_pcs = nullptr;
         }
-        std::pair<hipEvent_t, hipEvent_t> ev{};
+        if (stats_mode != 3) s.census = nullptr;
+        nesle_batch::Marks ev{};
         if (b->timing) {
             b->fold_events(false);
             ev = b->take_events();
-            hip_check(hipEventRecord(ev.first, b->stream), "hipEventRecord");
+            hip_check(hipEventRecord(ev.start, b->stream), "hipEventRecord");
         }
-        hip_check(nesle::launch_step(s, b->cfg.frameskip, b->cfg.max_instructions_per_frame, auto_reset != 0,
-                                     stats_mode, b->stream),
+        hip_check(nesle::launch_step(s, b->cfg.frameskip, b->cfg.max_instructions_per_frame, stats_mode, b->stream),
                   "step_kernel");
+        if (b->timing) hip_check(hipEventRecord(ev.stepped, b->stream), "hipEventRecord");
+        // Auto-reset: done consoles restored from their level's snapshot (or
+        // powered on); rewards and dones of the step stay as written, as the
+        // reference's last_rewards/last_done copies do (cuda_module.cu:635-656).
+        if (auto_reset != 0) hip_check(nesle::launch_reset(s, s.done, b->stream), "restore_kernel");
         if (b->timing) {
-            hip_check(hipEventRecord(ev.second, b->stream), "hipEventRecord");
+            hip_check(hipEventRecord(ev.reset, b->stream), "hipEventRecord");
             b->events.push_back(ev);
         }
         b->refresh_obs();
@@ -631,6 +652,7 @@ int nesle_get_view(nesle_batch* b, int kind, nesle_view* out) {
             case NESLE_VIEW_BUDGET_HITS: b->ensure_stats(); v.data = b->ds.stat_budget_hits; v.dtype = NESLE_DTYPE_U32; break;
             case NESLE_VIEW_OPCODES: b->ensure_stats(); v.data = b->ds.prof_opcodes; v.shape[0] = 256; v.dtype = NESLE_DTYPE_U64; break;
             case NESLE_VIEW_PCS: b->ensure_stats(); v.data = b->ds.prof_pcs; v.shape[0] = 65536; v.dtype = NESLE_DTYPE_U64; break;
+            case NESLE_VIEW_CENSUS: b->ensure_stats(); v.data = b->ds.census; v.shape[0] = nesle::census::kCount; v.dtype = NESLE_DTYPE_U64; break;
             case NESLE_VIEW_FRAME_RGB: frame(b->d_frame_rgb, 4, 240, 256, 3); break;
             case NESLE_VIEW_FRAME_PALETTE: frame(b->d_frame_palette, 3, 240, 256, 0); break;
             case NESLE_VIEW_GRAY84: frame(b->d_gray84, 3, nesle::render::kOut, nesle::render::kOut, 0); break;
@@ -805,16 +827,24 @@ int nesle_set_timing(nesle_batch* b, int enable) {
         b->fold_events(true);
         b->timing = enable != 0;
         b->timed_ms = 0.0;
+        b->timed_reset_ms = 0.0;
         b->timed_launches = 0;
+        // Events for the first timed steps exist before they are recorded.
+        while (b->timing && b->spare.size() < 4) b->spare.push_back(nesle_batch::new_marks());
     });
 }
 
 int nesle_get_timing(nesle_batch* b, double* total_ms, std::uint64_t* launches) {
+    return nesle_get_timing_split(b, total_ms, nullptr, launches);
+}
+
+int nesle_get_timing_split(nesle_batch* b, double* step_ms, double* reset_ms, std::uint64_t* launches) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
         b->activate();
         b->fold_events(true);
-        if (total_ms != nullptr) *total_ms = b->timed_ms;
+        if (step_ms != nullptr) *step_ms = b->timed_ms;
+        if (reset_ms != nullptr) *reset_ms = b->timed_reset_ms;
         if (launches != nullptr) *launches = b->timed_launches;
     });
 }

@@ -12,8 +12,9 @@
 namespace nesle {
 
 // stats_mode: 0 none, 1 per-console counters, 2 counters + opcode/PC histograms.
-hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr,
-                       bool auto_reset, int stats_mode, hipStream_t stream);
+// The auto-reset after a step is a separate launch_reset (below).
+hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
+                       hipStream_t stream);
 // Masked (null = all) reset from the snapshot bank, or power-on without one.
 // The auto-reset after a step is this launch with the step's done flags as
 // the mask.

@@ -124,6 +124,7 @@ struct DeviceState {
     std::uint32_t* stat_budget_hits;
     unsigned long long* prof_opcodes;  // [256]
     unsigned long long* prof_pcs;      // [65536]
+    unsigned long long* census;        // [census::kCount] (stats mode 3)
 
     // Snapshot bank: num_levels canonical blobs, env_to_level[n].
     const std::uint8_t* bank;
@@ -139,6 +140,43 @@ struct DeviceState {
     std::uint8_t* lat_sy;      // [n]
     std::uint8_t* lat_ctrl;    // [n]
 };
+
+// Step-kernel census (stats mode 3): what the waves of one launch did, summed
+// over waves.  A "wave-iteration" is one trip of the step loop (one emulated
+// instruction or NMI entry for each lane of the wave); a cause counts a
+// wave-iteration when at least one lane of the wave has it.  Cycle counts
+// come from the shader clock read at the ends of each section, so they
+// include the waits those reads add.
+namespace census {
+enum : std::uint32_t {
+    kWaves = 0,          // waves that ran the loop
+    kIterations,         // wave-iterations
+    kRare,               // ... that took the rare path (any cause below)
+    kRareIoWrite,        // I/O register or PRG RAM write
+    kRareSide,           // JMP ($xxxx), or stack bytes outside the LDS window
+    kRareIdle,           // JMP to itself (idle-loop fast-forward)
+    kRareIllegal,        // illegal opcode
+    kRareTiming,         // PPU timing event crossed
+    kRareBudget,         // per-frame instruction budget reached
+    kRareOutside,        // next instruction outside PRG ROM
+    kRareOnlyIoWrite,    // rare wave-iterations whose only cause is I/O writes
+    kDma,                // wave-iterations with an OAM DMA copy
+    kPresent,            // wave-iterations with a presentation capture
+    kIoRead,             // wave-iterations with an I/O or PRG RAM read
+    kIoReadSlow,         // ... through the branchy register read (not $2002/$4016)
+    kActiveLanes,        // sum over wave-iterations of lanes still running frames
+    kDistinctEntries,    // sum over wave-iterations of distinct microcode entries among those lanes
+    kCyclesLoop,         // shader clock, loop entry to exit, summed over waves
+    kCyclesRare,         // ... inside the rare path (including the decode redone after it)
+    kCyclesIoRead,       // ... inside the I/O read side path
+    kLanesIoWrite,       // lane events: I/O writes
+    kLanesTiming,        // lane events: timing events crossed
+    kLanesIoRead,        // lane events: I/O reads
+    kLanesIoReadSlow,    // lane events: I/O reads through the branchy path
+    kExits,              // rare wave-iterations after which the wave left the loop
+    kCount = 32
+};
+}  // namespace census
 
 // Video memory block of one console: palette, OAM, then 2 KB of nametable
 // RAM (4 KB on four-screen carts).  vram_stride = kNametable + nt_bytes.

@@ -486,8 +486,38 @@ struct Console {
     }
 };
 
+// Census of one wave (stats mode 3): wave-uniform counters built from ballots
+// and the shader clock, added to the launch's totals when the wave is done.
+struct WaveCensus {
+    std::uint64_t v[census::kCount] = {};
+    __device__ __forceinline__ void count(std::uint32_t k, bool any_lane) {
+        v[k] += __builtin_amdgcn_ballot_w64(any_lane) != 0 ? 1u : 0u;
+    }
+    __device__ __forceinline__ void lanes(std::uint32_t k, bool lane_has) {
+        v[k] += static_cast<std::uint64_t>(__popcll(__builtin_amdgcn_ballot_w64(lane_has)));
+    }
+    // Distinct values of `key` among the lanes in `who`.
+    __device__ __forceinline__ static std::uint32_t distinct(std::uint32_t key, bool who) {
+        std::uint64_t rem = __builtin_amdgcn_ballot_w64(who);
+        std::uint32_t k = 0;
+        while (rem != 0) {
+            const std::uint32_t first = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(rem)) - 1);
+            const std::uint32_t pick = __builtin_amdgcn_readlane(key, first);
+            rem &= ~__builtin_amdgcn_ballot_w64(key == pick);
+            ++k;
+        }
+        return k;
+    }
+    __device__ void flush(unsigned long long* out, std::uint32_t lane) const {
+        if (out == nullptr || lane != 0) return;
+        for (std::uint32_t k = 0; k < census::kCount; ++k)
+            if (v[k] != 0) atomicAdd(out + k, static_cast<unsigned long long>(v[k]));
+    }
+};
+
 // ---- the step kernel ---------------------------------------------------------------
-// kStats: 0 none, 1 per-console counters, 2 counters + opcode/PC histograms.
+// kStats: 0 none, 1 per-console counters, 2 counters + opcode/PC histograms,
+// 3 counters + the census of the launch (WaveCensus).
 // kFull: all console RAM in LDS.  kBudget: the per-frame instruction budget can
 // bind (a frame always completes within 14,891 instructions, since every
 // instruction advances the PPU by at least 6 dots).
@@ -638,6 +668,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         slices(active ? op : mc::kNopEntry);
         address(op, b1, b2, c.regs);
     }
+    [[maybe_unused]] WaveCensus cz;
+    [[maybe_unused]] std::uint64_t t_loop = 0, t_rare = 0;
+    if constexpr (kStats == 3) {
+        t_loop = clock64();
+        cz.count(census::kWaves, active);
+    }
     // The loop ends when no lane is active; lanes only stop in the rare work,
     // so only that path tests it.
     if (__builtin_amdgcn_ballot_w64(active) != 0) for (;;) {
@@ -724,6 +760,15 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const std::uint32_t m_lds = rom ? rom_v : ram_v;
         std::uint32_t M = (rd && (rom || ram_lds)) ? m_lds : b1;
         M = sel(d13, w1, M);
+        if constexpr (kStats == 3) {
+            const bool slow = rd && io && (ea & 0xE007) != 0x2002 && ea != 0x4016;
+            cz.count(census::kIoRead, rd && io);
+            cz.count(census::kIoReadSlow, slow);
+            cz.lanes(census::kLanesIoRead, rd && io);
+            cz.lanes(census::kLanesIoReadSlow, slow);
+        }
+        [[maybe_unused]] std::uint64_t t_io = 0;
+        if constexpr (kStats == 3) t_io = clock64();
         if (kFull) {
             if (rd && io) M = c.io_read(ea);   // all RAM is in LDS: no HBM operand
         } else {
@@ -734,6 +779,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             if (rd && io) mio = c.io_read(ea);
             M = (rd && io) ? mio : M;
             M = (rd && glob) ? gval : M;
+        }
+        if constexpr (kStats == 3) {
+            if (__builtin_amdgcn_ballot_w64(rd && io) != 0) cz.v[census::kCyclesIoRead] += clock64() - t_io;
         }
 
         // Adder, logic unit and right shifter.
@@ -806,6 +854,23 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const bool budget = kBudget && counted && in_frame >= max_instr;
         const bool rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
                           (next - 0x8000u) > 0x7FFDu;
+        if constexpr (kStats == 3) {
+            cz.v[census::kIterations] += 1;
+            cz.lanes(census::kActiveLanes, active);
+            cz.v[census::kDistinctEntries] += WaveCensus::distinct(mi, active);
+            cz.count(census::kRare, rare);
+            cz.count(census::kRareIoWrite, io_write);
+            cz.count(census::kRareSide, side);
+            cz.count(census::kRareIdle, idle);
+            cz.count(census::kRareIllegal, (d14 & mc::kIllegal) != 0);
+            cz.count(census::kRareTiming, timing);
+            cz.count(census::kRareBudget, budget);
+            cz.count(census::kRareOutside, (next - 0x8000u) > 0x7FFDu);
+            const bool others = side || idle || (d14 & mc::kIllegal) || timing || budget || (next - 0x8000u) > 0x7FFDu;
+            if (__builtin_amdgcn_ballot_w64(others) == 0) cz.count(census::kRareOnlyIoWrite, io_write);
+            cz.lanes(census::kLanesIoWrite, io_write);
+            cz.lanes(census::kLanesTiming, timing);
+        }
         if constexpr (!kFull) s.ram[c.goff((wr && glob) ? row : kTrashRow)] = static_cast<std::uint8_t>(r);
         if constexpr (!kFull) {   // decode of the next instruction
             ma_c = ma_n; me_c = me_n;
@@ -815,6 +880,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             left -= static_cast<std::int32_t>(dots);
             continue;
         }
+        if constexpr (kStats == 3) t_rare = clock64();
         if (io_write) dots += c.io_wr(ea, r);
         if (side) {
             std::uint32_t npc = next;
@@ -900,6 +966,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // pages have no read side effects; I/O pages are read by the console's
         // own lane through the bus, in order.
         std::uint64_t req = __ballot((c.flags & kDmaPending) != 0);
+        if constexpr (kStats == 3) cz.v[census::kDma] += req != 0 ? 1u : 0u;
         while (req != 0) {
             const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(req)) - 1);
             req &= req - 1;
@@ -941,6 +1008,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // OAM DMA of the same instruction: the wave copies one console's
         // video memory block at a time (dwords, contiguous) into its record.
         std::uint64_t preq = __ballot((c.flags & kPresentPending) != 0);
+        if constexpr (kStats == 3) cz.v[census::kPresent] += preq != 0 ? 1u : 0u;
         while (preq != 0) {
             const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(preq)) - 1);
             preq &= preq - 1;
@@ -954,13 +1022,27 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // a $2000 write or the vblank event): its entry runs next.
         if (active && !(c.flags & kNmiPending) && (c.pc - 0x8000u) > 0x7FFDu) fetch_bus();
         if (c.flags & kNmiPending) op = mc::kNmiEntry;
-        if (__builtin_amdgcn_ballot_w64(active) == 0) break;
+        if (__builtin_amdgcn_ballot_w64(active) == 0) {
+            if constexpr (kStats == 3) {
+                cz.v[census::kExits] += 1;
+                cz.v[census::kCyclesRare] += clock64() - t_rare;
+            }
+            break;
+        }
         if constexpr (!kFull) {
             // The rare work may have changed the next instruction, the
             // registers or RAM: decode again.
             slices(active ? op : mc::kNopEntry);
             address(op, b1, b2, c.regs);
         }
+        if constexpr (kStats == 3) {
+            vmem_settled();   // the redone decode's load is part of the rare cost
+            cz.v[census::kCyclesRare] += clock64() - t_rare;
+        }
+    }
+    if constexpr (kStats == 3) {
+        cz.v[census::kCyclesLoop] += clock64() - t_loop;
+        cz.flush(s.census, lane);
     }
 
     if (!mine) return;
@@ -1088,27 +1170,18 @@ std::uint32_t waves_per_group() {
 
 }  // namespace
 
-hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, bool auto_reset,
-                       int stats_mode, hipStream_t stream) {
+hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
+                       hipStream_t stream) {
     Geometry g = geometry(s.n, waves_per_group());
     if (g.full && g.waves != 4) g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
     if (g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
     // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
     const bool budget = max_instr < 15000;
-    hipError_t e;
-    if (stats_mode == 2) {
-        e = launch_mode<2, true>(s, g, frameskip, max_instr, stream);
-    } else if (stats_mode == 1) {
-        e = launch_mode<1, true>(s, g, frameskip, max_instr, stream);
-    } else {
-        e = budget ? launch_mode<0, true>(s, g, frameskip, max_instr, stream)
-                   : launch_mode<0, false>(s, g, frameskip, max_instr, stream);
-    }
-    if (e != hipSuccess || !auto_reset) return e;
-    // Auto-reset: done consoles restored from their level's snapshot (or
-    // powered on); rewards and dones of the step stay as written, as the
-    // reference's last_rewards/last_done copies do (cuda_module.cu:635-656).
-    return launch_reset(s, s.done, stream);
+    if (stats_mode == 3) return launch_mode<3, true>(s, g, frameskip, max_instr, stream);
+    if (stats_mode == 2) return launch_mode<2, true>(s, g, frameskip, max_instr, stream);
+    if (stats_mode == 1) return launch_mode<1, true>(s, g, frameskip, max_instr, stream);
+    return budget ? launch_mode<0, true>(s, g, frameskip, max_instr, stream)
+                  : launch_mode<0, false>(s, g, frameskip, max_instr, stream);
 }
 
 }  // namespace nesle

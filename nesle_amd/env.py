@@ -211,8 +211,14 @@ class _Observer:
         return np.where(which[:, None, None, None], self.frames, obs)
 
     def _ram_gather(self, rows: np.ndarray) -> np.ndarray:
-        import torch
-
+        """RAM rows of ``rows`` now: gathered on the device through the DLPack
+        view when torch is importable (only those rows cross PCIe), else from
+        a whole host copy, as the reference re-reads ``ram()`` (torch is an
+        optional dependency of the environment layer)."""
+        try:
+            import torch
+        except ImportError:
+            return self.batch.ram()[rows]
         if self._ram_dev is None:
             self._ram_dev = torch.from_dlpack(self.batch.ram_device())
         index = torch.as_tensor(rows, dtype=torch.long).to(self._ram_dev.device)

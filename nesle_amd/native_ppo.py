@@ -150,33 +150,27 @@ def _explained_variance(values, returns) -> float:
 
 
 # ---- checkpoints -----------------------------------------------------------
-# A checkpoint is a flat dict of tensors, numbers, strings and lists only, so
-# that torch.load(weights_only=True) reads it back without running pickled
-# code: model and optimizer state dicts, the config as a dict, the env-step
-# count, and the three RNG states (numpy's MT19937 as its key tensor plus
-# position and Gaussian cache).
+# A checkpoint keeps the reference trainer's top-level keys (native_ppo.py:
+# 319-368: model, optimizer, config, global_step, torch_rng_state,
+# cuda_rng_state, numpy_rng_state), so tools that read those names keep
+# working, but every value is a tensor, number, string or list: numpy's RNG
+# state is [name, key tensor, pos, has_gauss, cached], so that
+# torch.load(weights_only=True) reads the file back without running pickled
+# code.  Loading also accepts the layout that kept the RNG states under one
+# "rng" entry (format "nesle_amd.native_ppo/1").
 
-CHECKPOINT_FORMAT = "nesle_amd.native_ppo/1"
-
-
-def _rng_snapshot(torch) -> dict:
-    mt = np.random.get_state(legacy=False)
-    snap = {"torch": torch.get_rng_state(),
-            "numpy_key": torch.from_numpy(mt["state"]["key"].astype(np.int64)),
-            "numpy_pos": int(mt["state"]["pos"]), "numpy_has_gauss": int(mt["has_gauss"]),
-            "numpy_gauss": float(mt["gauss"])}
-    if torch.cuda.is_available():
-        snap["cuda"] = torch.cuda.get_rng_state()
-    return snap
+CHECKPOINT_FORMAT = "nesle_amd.native_ppo/2"
+_RNG_DICT_FORMAT = "nesle_amd.native_ppo/1"
 
 
-def _rng_restore(torch, snap: dict) -> None:
-    torch.set_rng_state(snap["torch"].cpu())
-    if "cuda" in snap and torch.cuda.is_available():
-        torch.cuda.set_rng_state(snap["cuda"].cpu())
-    np.random.set_state({"bit_generator": "MT19937",
-                         "state": {"key": snap["numpy_key"].cpu().numpy().astype(np.uint32), "pos": snap["numpy_pos"]},
-                         "has_gauss": snap["numpy_has_gauss"], "gauss": snap["numpy_gauss"]})
+def _numpy_rng_list(torch) -> list:
+    name, keys, pos, has_gauss, cached = np.random.get_state()
+    return [str(name), torch.from_numpy(np.asarray(keys, dtype=np.int64)), int(pos), int(has_gauss), float(cached)]
+
+
+def _set_numpy_rng(name, keys, pos, has_gauss, cached) -> None:
+    keys = keys.cpu().numpy() if hasattr(keys, "cpu") else np.asarray(keys)
+    np.random.set_state((str(name), keys.astype(np.uint32), int(pos), int(has_gauss), float(cached)))
 
 
 def _save_checkpoint(path: str, model, optimizer, config: NativePPOConfig, global_step: int) -> None:
@@ -184,11 +178,14 @@ def _save_checkpoint(path: str, model, optimizer, config: NativePPOConfig, globa
     plain = {}
     for key, value in asdict(config).items():
         plain[key] = list(value) if isinstance(value, tuple) else value
+    ckpt = {"model": model.state_dict(), "optimizer": optimizer.state_dict(), "config": plain,
+            "global_step": int(global_step), "torch_rng_state": torch.get_rng_state(),
+            "numpy_rng_state": _numpy_rng_list(torch), "format": CHECKPOINT_FORMAT}
+    if torch.cuda.is_available():
+        ckpt["cuda_rng_state"] = torch.cuda.get_rng_state()
     target = Path(path)
     target.resolve().parent.mkdir(parents=True, exist_ok=True)
-    torch.save({"format": CHECKPOINT_FORMAT, "global_step": int(global_step), "config": plain,
-                "model": model.state_dict(), "optimizer": optimizer.state_dict(), "rng": _rng_snapshot(torch)},
-               target)
+    torch.save(ckpt, target)
 
 
 def _load_checkpoint(path: str | None, model, optimizer) -> int:
@@ -199,11 +196,23 @@ def _load_checkpoint(path: str | None, model, optimizer) -> int:
     torch, _, _ = _require_torch()
     where = torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
     ckpt = torch.load(path, map_location=where, weights_only=True)
-    if ckpt.get("format") != CHECKPOINT_FORMAT:
-        raise ValueError(f"{path} is not a {CHECKPOINT_FORMAT} checkpoint")
+    if not all(k in ckpt for k in ("model", "optimizer", "global_step")):
+        raise ValueError(f"{path} is not a PPO checkpoint (needs model, optimizer and global_step)")
     model.load_state_dict(ckpt["model"])
     optimizer.load_state_dict(ckpt["optimizer"])
-    _rng_restore(torch, ckpt["rng"])
+    if ckpt.get("format") == _RNG_DICT_FORMAT:
+        rng = ckpt["rng"]
+        torch_state, cuda_state = rng["torch"], rng.get("cuda")
+        mt = ("MT19937", rng["numpy_key"], rng["numpy_pos"], rng["numpy_has_gauss"], rng["numpy_gauss"])
+    else:
+        torch_state, cuda_state = ckpt.get("torch_rng_state"), ckpt.get("cuda_rng_state")
+        mt = ckpt.get("numpy_rng_state")
+    if torch_state is not None:
+        torch.set_rng_state(torch_state.cpu())
+    if cuda_state is not None and torch.cuda.is_available():
+        torch.cuda.set_rng_state(cuda_state.cpu())
+    if mt is not None:
+        _set_numpy_rng(*mt)
     return int(ckpt["global_step"])
 
 
@@ -432,8 +441,9 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                      on_rollout=None) -> dict:
     """Train; returns {"global_step", "updates", "rollout_s", "update_s",
     "emulator_s", "wall_s", "log", "per_update", "graph_updates", "model"}
-    (emulator_s: step-kernel time per rollout step from HIP events on the
-    batch's stream during the eager first rollout, times the steps).
+    (emulator_s: step-kernel plus auto-reset restore-kernel time per rollout
+    step from HIP events on the batch's stream during the eager first
+    rollout, times the steps).
     ``record(step, masks, rewards, dones)`` receives each step's device tensors
     and keeps every rollout eager; ``on_rollout(update, buffers)`` receives
     the rollout buffers after each rollout (tests)."""
@@ -539,7 +549,7 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     stats = {"global_step": global_step, "updates": 0, "rollout_s": 0.0, "update_s": 0.0, "emulator_s": 0.0,
              "wall_s": 0.0, "log": [], "per_update": [], "graph_updates": 0}
     graph = None
-    step_ms = None   # step-kernel time per rollout step, from the eager first rollout
+    step_ms = None   # step + restore kernel time per rollout step, from the eager first rollout
     t_start = time.perf_counter()
     for update in range(1, num_updates + 1):
         # The first rollout runs eagerly (HIP-event timing of the step kernel,
@@ -565,9 +575,9 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         if not use_graph:
-            kernel_ms, launches = batch.kernel_timing()
+            kernel_ms, reset_ms, launches = batch.kernel_timing_split()
             batch.set_timing(False)
-            step_ms = kernel_ms / max(launches, 1)
+            step_ms = (kernel_ms + reset_ms) / max(launches, 1)   # step kernel + auto-reset restore
         else:
             stats["graph_updates"] += 1
         if on_rollout is not None:

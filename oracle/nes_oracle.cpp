@@ -1042,6 +1042,21 @@ void oracle_set_presentation(void* h, const std::uint8_t* f) {
     p.sx_start = f[0]; p.sy_start = f[1]; p.ctrl_start = f[2];
     p.sx_end = f[3]; p.sy_end = f[4]; p.ctrl_end = f[5]; p.mask = f[6];
 }
+// The presentation state, laid out as the reference harness's
+// ref_present_get: [0..6] frame-start x, y, ctrl, frame-end x, y, ctrl, mask;
+// [7..9] the pre-render latch x, y, ctrl; [16..271] OAM; [272..303] palette;
+// [304..2351] the first 2,048 bytes of nametable RAM.
+void oracle_present_get(void* h, std::uint8_t* out) {
+    const auto& m = static_cast<Env*>(h)->m;
+    const auto& p = m.snap;
+    const std::uint8_t head[10] = {p.sx_start, p.sy_start, p.ctrl_start, p.sx_end, p.sy_end,
+                                   p.ctrl_end, p.mask, m.lat_sx, m.lat_sy, m.lat_ctrl};
+    std::memset(out, 0, 16);
+    std::memcpy(out, head, 10);
+    std::memcpy(out + 16, p.oam, 256);
+    std::memcpy(out + 272, p.palette, 32);
+    std::memcpy(out + 304, p.nt, 2048);
+}
 void oracle_palette_rgb(std::uint8_t* out) { std::memcpy(out, kNesRgb, sizeof(kNesRgb)); }
 void oracle_gray84(const std::uint8_t* frame, std::uint8_t* out) { gray84(frame, out); }
 std::uint64_t oracle_splitmix64(std::uint64_t x) { return splitmix64(x); }

@@ -47,6 +47,10 @@ SECTIONS = {
 
 _U8P = ctypes.POINTER(ctypes.c_uint8)
 
+# Presentation state as Oracle.presentation / RefConsole.presentation lay it out.
+PRESENT_BYTES = 2352
+PRESENT_OFF = {"fields": 0, "latch": 7, "oam": 16, "palette": 272, "nametable": 304}
+
 
 def build(ref: bool = False) -> None:
     """Compile the oracle (and, if asked, the reference harness) with make."""
@@ -116,6 +120,7 @@ def _oracle_lib():
         lib.oracle_render.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _U8P]
         lib.oracle_seed_presentation.argtypes = [ctypes.c_void_p]
         lib.oracle_set_presentation.argtypes = [ctypes.c_void_p, _U8P]
+        lib.oracle_present_get.argtypes = [ctypes.c_void_p, _U8P]
         lib.oracle_palette_rgb.argtypes = [_U8P]
         lib.oracle_gray84.argtypes = [_U8P, _U8P]
         lib.oracle_run_batch.restype = ctypes.c_double
@@ -151,6 +156,12 @@ def _ref_lib():
         lib.ref_step_instruction.restype = ctypes.c_int64
         lib.ref_step_instruction.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32)]
         lib.ref_render_rgb.argtypes = [ctypes.c_void_p, _U8P]
+        lib.ref_present_seed.argtypes = [ctypes.c_void_p]
+        lib.ref_present_step.restype = ctypes.c_int64
+        lib.ref_present_step.argtypes = [ctypes.c_void_p, ctypes.c_uint8, ctypes.c_uint32, ctypes.c_uint64]
+        lib.ref_present_get.argtypes = [ctypes.c_void_p, _U8P]
+        lib.ref_batch_render.argtypes = [_U8P, ctypes.c_uint32, ctypes.c_uint32, _U8P, _U8P, _U8P, _U8P,
+                                         ctypes.c_uint32, _U8P]
         lib.ref_run_batch.restype = ctypes.c_double
         lib.ref_run_batch.argtypes = _oracle_lib().oracle_run_batch.argtypes
         lib.ref_run_levels.restype = ctypes.c_double
@@ -228,6 +239,14 @@ class Oracle:
     def seed_presentation(self) -> None:
         self.lib.oracle_seed_presentation(self.h)
 
+    def presentation(self) -> np.ndarray:
+        """The presentation state (PRESENT_BYTES): frame-start x, y, ctrl,
+        frame-end x, y, ctrl, mask, the pre-render latch x, y, ctrl, then OAM,
+        palette and the first 2,048 bytes of nametable RAM (PRESENT_OFF)."""
+        out = np.empty(PRESENT_BYTES, dtype=np.uint8)
+        self.lib.oracle_present_get(self.h, out.ctypes.data_as(_U8P))
+        return out
+
     def set_presentation(self, sx_start: int, sy_start: int, ctrl_start: int, sx_end: int, sy_end: int,
                          ctrl_end: int, mask: int) -> None:
         f = np.array([sx_start, sy_start, ctrl_start, sx_end, sy_end, ctrl_end, mask], dtype=np.uint8)
@@ -276,6 +295,45 @@ class RefConsole:
         out = np.empty((240, 256, 3), dtype=np.uint8)
         self.lib.ref_render_rgb(self.h, out.ctypes.data_as(_U8P))
         return out
+
+    def present_seed(self) -> None:
+        """Seed the batched core's presentation state from live state."""
+        self.lib.ref_present_seed(self.h)
+
+    def present_step(self, buttons: int, frameskip: int = 1, max_instructions: int = 200000) -> int:
+        """One env-step in which every instruction's dots also advance the
+        batched core's PPU timing (batch_ppu_step_env_hot); returns
+        instructions."""
+        n = self.lib.ref_present_step(self.h, buttons & 0xFF, frameskip, max_instructions)
+        if n < 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        return n
+
+    def presentation(self) -> np.ndarray:
+        """The batched core's presentation state, laid out as Oracle.presentation."""
+        out = np.empty(PRESENT_BYTES, dtype=np.uint8)
+        self.lib.ref_present_get(self.h, out.ctypes.data_as(_U8P))
+        return out
+
+
+def ref_batch_render(chr_rom: bytes, arrangement: int, fields, oam: np.ndarray, nametable: np.ndarray,
+                     palette: np.ndarray, snapshot: bool = True, per_pixel: bool = False) -> np.ndarray:
+    """The reference batched core's RGB frame (240, 256, 3) of one console
+    given directly (oracle/_ref, batch_render.cuh): `fields` = frame-start
+    x, y, ctrl, frame-end x, y, ctrl, mask; nametable of 4,096 bytes; CHR RAM
+    when `chr_rom` is empty.  `snapshot` False: live state (frame-end values,
+    no split); `per_pixel`: the per-pixel renderer of its device kernel."""
+    chr_arr = np.frombuffer(bytes(chr_rom) or b"\0", dtype=np.uint8).copy()
+    f = np.ascontiguousarray(fields, dtype=np.uint8)
+    o = np.ascontiguousarray(oam, dtype=np.uint8)
+    n = np.ascontiguousarray(nametable, dtype=np.uint8)
+    p = np.ascontiguousarray(palette, dtype=np.uint8)
+    assert f.size == 7 and o.size == 256 and n.size == 4096 and p.size == 32
+    out = np.empty((240, 256, 3), dtype=np.uint8)
+    _ref_lib().ref_batch_render(chr_arr.ctypes.data_as(_U8P), len(chr_rom), arrangement, f.ctypes.data_as(_U8P),
+                                o.ctypes.data_as(_U8P), n.ctypes.data_as(_U8P), p.ctypes.data_as(_U8P),
+                                (1 if snapshot else 0) | (2 if per_pixel else 0), out.ctypes.data_as(_U8P))
+    return out
 
 
 def palette_rgb() -> np.ndarray:

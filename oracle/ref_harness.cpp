@@ -34,15 +34,32 @@
 #include "nesle/console.hpp"
 #include "nesle/rom.hpp"
 #undef private
+// The batched core's PPU timing and renderer, compiled as host C++ (the
+// reference's own host tests do the same, tests/cpp/test_cuda_render.cpp).
+#include "nesle/cuda/batch_ppu.cuh"
+#include "nesle/cuda/batch_render.cuh"
 
 namespace {
 
 constexpr std::size_t kStateBytes = 22896;
 
+// The batched core's presentation state of one console, advanced beside the
+// CPU core by batch_ppu_step_env_hot (batch_ppu.cuh:183-269) with the
+// console's registers and video memory after each instruction: the frame-start
+// latch (lat_*) and the vblank snapshot (snap_*).
+struct Shadow {
+    std::uint8_t lat_sx = 0, lat_sy = 0, lat_ctrl = 0;
+    std::uint8_t sx_start = 0, sy_start = 0, ctrl_start = 0, sx_end = 0, sy_end = 0, ctrl_end = 0, mask = 0;
+    std::array<std::uint8_t, 256> oam{};
+    std::array<std::uint8_t, 2048> nt{};
+    std::array<std::uint8_t, 32> palette{};
+};
+
 struct RefEnv {
     explicit RefEnv(nesle::RomImage rom) : console(std::move(rom)) { console.reset_cpu(cpu); }
     nesle::Console console;
     nesle::cpu::CpuState cpu;
+    Shadow shadow;
 };
 
 thread_local std::string g_error;
@@ -304,6 +321,162 @@ double ref_run_levels(const std::uint8_t* ines, std::size_t len, const std::uint
     if (instructions) *instructions = instr.load();
     if (resets) *resets = rs.load();
     return secs;
+}
+
+
+// ---- the batched core's frame path (batch_ppu.cuh, batch_render.cuh) ----------
+
+// Presentation state seeded from live state, as a full reset of the batched
+// core does (cuda_module.cu:1440-1463).
+void ref_present_seed(void* h) {
+    auto* e = static_cast<RefEnv*>(h);
+    const auto& p = e->console.ppu_;
+    auto& sh = e->shadow;
+    sh.lat_sx = sh.sx_start = sh.sx_end = p.scroll_x_;
+    sh.lat_sy = sh.sy_start = sh.sy_end = p.scroll_y_;
+    sh.lat_ctrl = sh.ctrl_start = sh.ctrl_end = p.ctrl_;
+    sh.mask = p.mask_;
+    std::memcpy(sh.oam.data(), p.oam_.data(), 256);
+    std::memcpy(sh.nt.data(), p.nametable_ram_.data(), 2048);
+    std::memcpy(sh.palette.data(), p.palette_ram_.data(), 32);
+}
+
+// One env-step of the CPU core (Console::step_frame, console.hpp:137-150,
+// `frameskip` times) in which every instruction's PPU dots also advance the
+// batched core's timing (batch_ppu_step_env_hot) over a one-console
+// BatchBuffers that points at the console's registers and video memory as the
+// instruction left them -- the batched core's order: the instruction's
+// register writes, then its dots.  Returns instructions, -1 on an exception.
+std::int64_t ref_present_step(void* h, std::uint8_t buttons, std::uint32_t frameskip, std::uint64_t max_instructions) {
+    auto* e = static_cast<RefEnv*>(h);
+    auto& c = e->console;
+    auto& p = c.ppu_;
+    auto& sh = e->shadow;
+    std::uint8_t ctrl = 0, mask = 0, status = 0, oam_addr = 0, nmi = 0, sx = 0, sy = 0;
+    std::uint32_t frame_dot = static_cast<std::uint32_t>(p.scanline_) * 341u + p.dot_;
+    std::uint64_t frame_count = p.frame_;
+    nesle::cuda::BatchBuffers b{};
+    b.ppu.ctrl = &ctrl;
+    b.ppu.mask = &mask;
+    b.ppu.status = &status;
+    b.ppu.oam_addr = &oam_addr;
+    b.ppu.nmi_pending = &nmi;
+    b.ppu.frame_dot = &frame_dot;
+    b.ppu.frame = &frame_count;
+    b.ppu.scroll_x = &sx;
+    b.ppu.scroll_y = &sy;
+    b.ppu.oam = p.oam_.data();
+    b.ppu.nametable_ram = p.nametable_ram_.data();
+    b.ppu.palette_ram = p.palette_ram_.data();
+    b.ppu.lat_scroll_x = &sh.lat_sx;
+    b.ppu.lat_scroll_y = &sh.lat_sy;
+    b.ppu.lat_ctrl = &sh.lat_ctrl;
+    b.ppu.snap_scroll_x_start = &sh.sx_start;
+    b.ppu.snap_scroll_y_start = &sh.sy_start;
+    b.ppu.snap_ctrl_start = &sh.ctrl_start;
+    b.ppu.snap_scroll_x_end = &sh.sx_end;
+    b.ppu.snap_scroll_y_end = &sh.sy_end;
+    b.ppu.snap_ctrl_end = &sh.ctrl_end;
+    b.ppu.snap_mask = &sh.mask;
+    b.ppu.snap_oam = sh.oam.data();
+    b.ppu.snap_nametable = sh.nt.data();
+    b.ppu.snap_palette = sh.palette.data();
+    try {
+        c.controller1().set_buttons(buttons);
+        std::int64_t n = 0;
+        for (std::uint32_t f = 0; f < frameskip; ++f) {
+            for (std::uint64_t i = 0; i < max_instructions; ++i) {
+                const auto r = c.step_cpu_instruction(e->cpu);
+                ++n;
+                nesle::cuda::PpuHotState hot;
+                hot.frame_dot = frame_dot;
+                hot.frame = frame_count;
+                hot.ctrl = p.ctrl_;
+                hot.mask = p.mask_;
+                sx = p.scroll_x_;
+                sy = p.scroll_y_;
+                nesle::cuda::batch_ppu_step_env_hot(b, 0, r.ppu_cycles, hot);
+                frame_dot = hot.frame_dot;
+                frame_count = hot.frame;
+                if (r.frames_completed != 0) break;
+            }
+        }
+        return n;
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1;
+    }
+}
+
+// The shadow presentation state: [0..6] frame-start x, y, ctrl, frame-end
+// x, y, ctrl, mask; [7..9] the latch x, y, ctrl; [16..271] OAM; [272..303]
+// palette; [304..2351] nametable RAM.
+void ref_present_get(void* h, std::uint8_t* out) {
+    const auto& sh = static_cast<RefEnv*>(h)->shadow;
+    const std::uint8_t head[10] = {sh.sx_start, sh.sy_start, sh.ctrl_start, sh.sx_end, sh.sy_end,
+                                   sh.ctrl_end, sh.mask, sh.lat_sx, sh.lat_sy, sh.lat_ctrl};
+    std::memset(out, 0, 16);
+    std::memcpy(out, head, 10);
+    std::memcpy(out + 16, sh.oam.data(), 256);
+    std::memcpy(out + 272, sh.palette.data(), 32);
+    std::memcpy(out + 304, sh.nt.data(), 2048);
+}
+
+// One frame of the batched core's renderer (batch_render.cuh:161-440) for
+// one console whose state is given directly: CHR ROM (chr_size 0 = CHR RAM,
+// which that renderer reads as 0), the nametable arrangement (0 vertical,
+// 1 horizontal, 2 four-screen), f = frame-start x, y, ctrl, frame-end x, y,
+// ctrl, mask, and OAM (256), nametable RAM (4,096 bytes: four-screen reads
+// all of it) and palette RAM (32).  mode bit 0: from a presentation snapshot
+// holding these (render_batch_rgb_frame_env through
+// resolve_render_env_views), else from live state with the frame-end
+// scroll/ctrl and no snapshot; bit 1: the per-pixel renderer
+// (render_batch_rgb_pixel_env, what the reference's device kernel runs)
+// instead of the serial frame renderer.  out: 240 x 256 x RGB.
+void ref_batch_render(const std::uint8_t* chr, std::uint32_t chr_size, std::uint32_t arrangement,
+                      const std::uint8_t* f, const std::uint8_t* oam, const std::uint8_t* nt,
+                      const std::uint8_t* palette, std::uint32_t mode, std::uint8_t* out) {
+    std::vector<std::uint8_t> chr_copy(chr, chr + chr_size);
+    std::array<std::uint8_t, 256> oam_copy{};
+    std::array<std::uint8_t, 4096> nt_copy{};
+    std::array<std::uint8_t, 32> pal_copy{};
+    std::memcpy(oam_copy.data(), oam, 256);
+    std::memcpy(nt_copy.data(), nt, 4096);
+    std::memcpy(pal_copy.data(), palette, 32);
+    std::uint8_t sx_start = f[0], sy_start = f[1], ctrl_start = f[2], sx_end = f[3], sy_end = f[4], ctrl_end = f[5];
+    std::uint8_t mask = f[6];
+    std::uint8_t live_ctrl = ctrl_end, live_mask = mask, live_sx = sx_end, live_sy = sy_end;
+    nesle::cuda::BatchBuffers b{};
+    b.cart.chr_rom = chr_size != 0 ? chr_copy.data() : nullptr;
+    b.cart.chr_rom_size = chr_size;
+    b.cart.nametable_arrangement = static_cast<std::uint8_t>(arrangement);
+    b.ppu.ctrl = &live_ctrl;
+    b.ppu.mask = &live_mask;
+    b.ppu.scroll_x = &live_sx;
+    b.ppu.scroll_y = &live_sy;
+    b.ppu.oam = oam_copy.data();
+    b.ppu.nametable_ram = nt_copy.data();
+    b.ppu.palette_ram = pal_copy.data();
+    if (mode & 1) {
+        b.ppu.snap_scroll_x_start = &sx_start;
+        b.ppu.snap_scroll_y_start = &sy_start;
+        b.ppu.snap_ctrl_start = &ctrl_start;
+        b.ppu.snap_scroll_x_end = &sx_end;
+        b.ppu.snap_scroll_y_end = &sy_end;
+        b.ppu.snap_ctrl_end = &ctrl_end;
+        b.ppu.snap_mask = &mask;
+        b.ppu.snap_oam = oam_copy.data();
+        b.ppu.snap_nametable = nt_copy.data();
+        b.ppu.snap_palette = pal_copy.data();
+    }
+    b.frames_rgb = out;
+    if (mode & 2) {
+        auto views = nesle::cuda::resolve_render_env_views(b, 0);
+        for (std::uint32_t px = 0; px < 240u * 256u; ++px)
+            nesle::cuda::render_batch_rgb_pixel_env(b, views.hud, views.play, 0, views.split_y, px);
+    } else {
+        nesle::cuda::render_batch_rgb_frame_env(b, 0);
+    }
 }
 
 }  // extern "C"

@@ -70,3 +70,30 @@ def test_gzip_reset_states_are_unpacked(tmp_path):
     q = tmp_path / "plain.fcs"
     q.write_bytes(raw)
     assert E.read_state_file(q) == raw
+
+
+def test_ram_rows_of_reset_consoles_without_torch(monkeypatch):
+    """Without torch the observation reader takes the rows of reset consoles
+    from a whole host copy of RAM (the reference env needs only numpy)."""
+    import sys
+
+    class FakeBatch:
+        def __init__(self):
+            self.ram_calls = 0
+
+        def ram(self):
+            self.ram_calls += 1
+            return np.arange(4 * 2048, dtype=np.int64).reshape(4, 2048).astype(np.uint8) + 7
+
+        def ram_device(self):  # pragma: no cover - must not be reached
+            raise AssertionError("device view used without torch")
+
+    monkeypatch.setitem(sys.modules, "torch", None)   # import torch -> ImportError
+    batch = FakeBatch()
+    obs_reader = E._Observer(batch, "ram", 1)
+    obs = np.zeros((4, 2048), dtype=np.uint8)
+    which = np.array([False, True, False, True])
+    out = obs_reader.replace_rows(obs, which)
+    full = batch.ram()
+    assert np.array_equal(out[1], full[1]) and np.array_equal(out[3], full[3])
+    assert not out[0].any() and not out[2].any()

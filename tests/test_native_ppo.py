@@ -174,10 +174,47 @@ def test_explained_variance_closed_forms():
     assert np.isnan(P._explained_variance(torch.rand(10), torch.ones(10)))
 
 
-def test_checkpoint_from_another_format_is_refused(tmp_path):
+def test_checkpoint_without_model_or_optimizer_is_refused(tmp_path):
     path = tmp_path / "other.pt"
     torch.save({"model": {}, "global_step": 3}, path)
     model = torch.nn.Linear(2, 2)
     with pytest.raises(ValueError, match="checkpoint"):
         P._load_checkpoint(str(path), model, torch.optim.Adam(model.parameters()))
     assert P._load_checkpoint(str(tmp_path / "missing.pt"), model, torch.optim.Adam(model.parameters())) == 0
+
+
+def test_checkpoint_keeps_the_reference_key_names(tmp_path):
+    """Top-level keys as the reference trainer writes them (native_ppo.py:
+    319-368), every value loadable with weights_only=True."""
+    model = torch.nn.Linear(3, 2)
+    opt = torch.optim.Adam(model.parameters())
+    path = tmp_path / "ckpt.pt"
+    P._save_checkpoint(str(path), model, opt, P.NativePPOConfig("rom.nes"), 5)
+    ckpt = torch.load(path, weights_only=True)
+    assert {"model", "optimizer", "config", "global_step", "torch_rng_state", "numpy_rng_state"} <= set(ckpt)
+    name, keys, pos, has_gauss, cached = ckpt["numpy_rng_state"]
+    assert name == "MT19937" and keys.shape == (624,) and 0 <= pos <= 624
+    assert ckpt["config"]["rom_path"] == "rom.nes" and ckpt["global_step"] == 5
+
+
+def test_checkpoint_of_the_earlier_layout_still_loads(tmp_path):
+    """Files of the layout that kept the RNG states under one "rng" entry
+    (format nesle_amd.native_ppo/1) resume: weights, step count and RNGs."""
+    model = torch.nn.Linear(4, 2)
+    opt = torch.optim.Adam(model.parameters())
+    np.random.seed(9)
+    torch.manual_seed(9)
+    mt = np.random.get_state(legacy=False)
+    old = {"format": "nesle_amd.native_ppo/1", "global_step": 321, "config": {}, "model": model.state_dict(),
+           "optimizer": opt.state_dict(),
+           "rng": {"torch": torch.get_rng_state(), "numpy_key": torch.from_numpy(mt["state"]["key"].astype(np.int64)),
+                   "numpy_pos": int(mt["state"]["pos"]), "numpy_has_gauss": int(mt["has_gauss"]),
+                   "numpy_gauss": float(mt["gauss"])}}
+    path = tmp_path / "old.pt"
+    torch.save(old, path)
+    a_t, a_n = torch.rand(3), np.random.rand(3)
+    model2 = torch.nn.Linear(4, 2)
+    assert P._load_checkpoint(str(path), model2, torch.optim.Adam(model2.parameters())) == 321
+    torch.testing.assert_close(model2.weight, model.weight)
+    torch.testing.assert_close(torch.rand(3), a_t)
+    np.testing.assert_allclose(np.random.rand(3), a_n)
