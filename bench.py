@@ -8,9 +8,11 @@ console auto-resets from one of 8 snapshots captured after 100-800 seeded
 warm-up frames (per-env level drawn uniformly); reward = clip(dx, -15, 15) -
 0.01 on the ROM's 16-bit x position.  The 4,096-console configuration (no
 resets) is timed in the same run and reported under "extra", and so is the
-pixel-observation workload: 16,384 consoles, each step followed by one render
-of every console's 84x84 gray observation into device memory (100 steps by
-default; the full 2,000 take ``--pixel-steps 2000``), and the GPU-resident PPO
+pixel-observation workload: 16,384 consoles on the status-bar variant of the
+ROM (sprite-0 timed, IRQ-free mid-frame $2005 writes, so frames start and end
+with different scrolls), each step followed by one render of every console's
+84x84 gray observation into device memory (100 steps by default; the full
+2,000 take ``--pixel-steps 2000``), and the GPU-resident PPO
 workload: 8,192 consoles x 128 steps per update on the snapshot/x-delta setup,
 RAM MLP policy (12-way action space, Xavier init), GAE and 4 epochs of
 minibatch 8,192, with the step kernel's share of the update's wall time; and
@@ -576,8 +578,9 @@ def main() -> int:
     pixel = None
     if args.pixel_steps > 0:
         log(f"timing {args.pixel_envs} envs x {args.pixel_steps} steps with an 84x84 gray frame per step")
-        pixel = run_gpu(core, rom, args.pixel_envs, args.pixel_steps, max(5, args.warmup // 4), None, None,
-                        gray84=True)
+        pixel = run_gpu(core, synthrom.make_rom(ROM_SEED, split=True).rom, args.pixel_envs, args.pixel_steps,
+                        max(5, args.warmup // 4), None, None, gray84=True)
+        pixel["rom"] = "status-bar variant of the seed-2026 ROM (sprite-0 timed mid-frame $2005 writes)"
         log(f"  {pixel['env_steps_per_s']:.0f} env-steps/s (pixel observations)")
 
     kernel_s = big["kernel_ms_per_launch"] / 1000.0

@@ -56,14 +56,19 @@ enum {
     NESLE_VIEW_FRAME_PALETTE = 11, /* uint8 [num_envs][240][256] palette values 0-63 */
     NESLE_VIEW_GRAY84 = 12,      /* uint8  [num_envs][84][84] gray observation */
     NESLE_VIEW_CENSUS = 13,      /* uint64 [32] step-kernel census (after stats mode 3 steps) */
-    NESLE_VIEW_COUNT = 14
+    NESLE_VIEW_PRESENT = 14,     /* uint8  [num_envs][16 + video memory block] presentation records:
+                                    frame-start x, y, ctrl, frame-end x, y, ctrl, mask, 9 spare
+                                    bytes, then palette, OAM and nametable RAM as frozen at the last
+                                    vblank (what nesle_render draws); frames on only */
+    NESLE_VIEW_COUNT = 15
 };
 
 /* nesle_render outputs (bit mask). */
 enum {
     NESLE_FRAME_RGB = 1,
     NESLE_FRAME_PALETTE = 2,
-    NESLE_FRAME_GRAY84 = 4
+    NESLE_FRAME_GRAY84 = 4,
+    NESLE_FRAME_LIVE = 8    /* modifier: draw live state with the CPU core's rules (see nesle_render) */
 };
 
 enum { NESLE_DTYPE_U8 = 0, NESLE_DTYPE_I64 = 1, NESLE_DTYPE_F32 = 2, NESLE_DTYPE_U32 = 3, NESLE_DTYPE_U64 = 4 };
@@ -174,7 +179,13 @@ int nesle_copy_to_host(nesle_batch* b, int kind, void* dst, size_t bytes);
  * (batch_render.cuh:161-440, launched by render_device/launch_render_device,
  * cuda_module.cu:1435-1438, 865-869); GRAY84 is the 84x84 luma observation
  * of the reference's training wrappers (project/mario-rl-ram/src/mario_rl/
- * wrappers.py:209-215, Pillow BILINEAR).  Fails with NESLE_EINVAL on a
+ * wrappers.py:209-215, Pillow BILINEAR).  With NESLE_FRAME_LIVE the frames
+ * are drawn instead from every console's live state by the rules of the
+ * reference CPU core's renderer (ppu.hpp:213-545, the frame its Console shows
+ * and per-frame framebuffer hashes are taken of): current scroll, ctrl, mask,
+ * OAM, palette and nametables, one scroll for the whole frame, a background
+ * pixel opaque whenever its pattern colour is non-zero, CHR RAM read; the
+ * presentation snapshot is left as it is.  Fails with NESLE_EINVAL on a
  * batch created with frames = 0.  Does not synchronise. */
 int nesle_render(nesle_batch* b, uint32_t outputs);
 

@@ -27,12 +27,14 @@ VIEW_RAM, VIEW_REWARDS, VIEW_DONES, VIEW_ACTIONS = 0, 1, 2, 3
 VIEW_INSTRUCTIONS, VIEW_FRAMES, VIEW_BUDGET_HITS, VIEW_OPCODES, VIEW_PCS, VIEW_OAM = 4, 5, 6, 7, 8, 9
 VIEW_FRAME_RGB, VIEW_FRAME_PALETTE, VIEW_GRAY84 = 10, 11, 12
 VIEW_CENSUS = 13
+VIEW_PRESENT = 14   # presentation records [n][16 + video memory block]
 # Step-kernel census slots (nesle_amd/csrc/nes_layout.h, namespace census).
 CENSUS_FIELDS = ("waves", "iterations", "rare", "rare_io_write", "rare_side", "rare_idle", "rare_illegal",
                  "rare_timing", "rare_budget", "rare_outside", "rare_only_io_write", "dma", "present", "io_read",
                  "io_read_slow", "active_lanes", "distinct_entries", "cycles_loop", "cycles_rare", "cycles_io_read",
                  "lanes_io_write", "lanes_timing", "lanes_io_read", "lanes_io_read_slow", "exits")
 FRAME_RGB, FRAME_PALETTE, FRAME_GRAY84 = 1, 2, 4
+FRAME_LIVE = 8      # modifier: live state under the reference CPU core's rules
 DTYPE_U8, DTYPE_I64, DTYPE_F32, DTYPE_U32, DTYPE_U64 = 0, 1, 2, 3, 4
 STATE_BYTES = 22896
 MAX_ENVS = 262144   # NESLE_MAX_ENVS
@@ -254,6 +256,11 @@ class Batch:
         return v
 
     def host(self, kind: int) -> np.ndarray:
+        if kind == VIEW_PRESENT:
+            v = self.view(kind)
+            out = np.empty((self.n, int(v.shape[1])), dtype=np.uint8)
+            _check(lib().nesle_copy_to_host(self.h, kind, out.ctypes.data, out.nbytes))
+            return out
         dt = {VIEW_RAM: (np.uint8, (self.n, 2048)), VIEW_REWARDS: (np.float32, (self.n,)),
               VIEW_DONES: (np.uint8, (self.n,)), VIEW_ACTIONS: (np.uint8, (self.n,)),
               VIEW_INSTRUCTIONS: (np.uint64, (self.n,)), VIEW_FRAMES: (np.uint32, (self.n,)),

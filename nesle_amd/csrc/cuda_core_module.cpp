@@ -291,9 +291,11 @@ public:
     }
 
     // One render launch producing any of the device outputs.
-    void render_frames_device(bool rgb, bool palette, bool gray84) {
+    // live: draw live state by the reference CPU core's rules (ppu.hpp:
+    // 213-545) instead of the presentation snapshot by the batched core's.
+    void render_frames_device(bool rgb, bool palette, bool gray84, bool live) {
         const std::uint32_t outputs = (rgb ? NESLE_FRAME_RGB : 0u) | (palette ? NESLE_FRAME_PALETTE : 0u) |
-                                      (gray84 ? NESLE_FRAME_GRAY84 : 0u);
+                                      (gray84 ? NESLE_FRAME_GRAY84 : 0u) | (live ? NESLE_FRAME_LIVE : 0u);
         check(nesle_render(h_, outputs));
     }
 
@@ -594,9 +596,9 @@ PYBIND11_MODULE(_cuda_core_native, m) {
                  return b.step_stats(a, 2);
              }, py::arg("actions"))
         .def("render", &CudaBatch::render)
-        .def("render_device", [](CudaBatch& b) { b.render_frames_device(true, false, false); })
+        .def("render_device", [](CudaBatch& b) { b.render_frames_device(true, false, false, false); })
         .def("render_frames_device", &CudaBatch::render_frames_device, py::arg("rgb") = true,
-             py::arg("palette") = false, py::arg("gray84") = false)
+             py::arg("palette") = false, py::arg("gray84") = false, py::arg("live") = false)
         .def("frames_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_FRAME_RGB); })
         .def("palette_frames_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_FRAME_PALETTE); })
         .def("gray84_device", [](const CudaBatch& b) { return b.view(NESLE_VIEW_GRAY84); })

@@ -226,6 +226,7 @@ struct nesle_batch {
     std::uint8_t* d_frame_rgb = nullptr;
     std::uint8_t* d_frame_palette = nullptr;
     std::uint8_t* d_gray84 = nullptr;
+    std::uint8_t* d_live_records = nullptr;   // records of live state (NESLE_FRAME_LIVE renders)
     void* d_render_tables = nullptr;   // render::Tables
     // Step timing: three events per step (before the step kernel, between it
     // and the auto-reset's restore kernel, after that), folded into the
@@ -252,6 +253,7 @@ struct nesle_batch {
         (void)hipFree(d_frame_rgb);
         (void)hipFree(d_frame_palette);
         (void)hipFree(d_gray84);
+        (void)hipFree(d_live_records);
         (void)hipFree(d_render_tables);
     }
 
@@ -652,6 +654,11 @@ int nesle_get_view(nesle_batch* b, int kind, nesle_view* out) {
             case NESLE_VIEW_BUDGET_HITS: b->ensure_stats(); v.data = b->ds.stat_budget_hits; v.dtype = NESLE_DTYPE_U32; break;
             case NESLE_VIEW_OPCODES: b->ensure_stats(); v.data = b->ds.prof_opcodes; v.shape[0] = 256; v.dtype = NESLE_DTYPE_U64; break;
             case NESLE_VIEW_PCS: b->ensure_stats(); v.data = b->ds.prof_pcs; v.shape[0] = 65536; v.dtype = NESLE_DTYPE_U64; break;
+            case NESLE_VIEW_PRESENT:
+                if (b->ds.present == nullptr) throw InvalidArgument("frames are off for this batch (created with frames = 0)");
+                v.data = b->ds.present; v.ndim = 2; v.shape[1] = nesle::present::kHeader + b->ds.vram_stride;
+                v.dtype = NESLE_DTYPE_U8;
+                break;
             case NESLE_VIEW_CENSUS: b->ensure_stats(); v.data = b->ds.census; v.shape[0] = nesle::census::kCount; v.dtype = NESLE_DTYPE_U64; break;
             case NESLE_VIEW_FRAME_RGB: frame(b->d_frame_rgb, 4, 240, 256, 3); break;
             case NESLE_VIEW_FRAME_PALETTE: frame(b->d_frame_palette, 3, 240, 256, 0); break;
@@ -690,7 +697,9 @@ int nesle_copy_to_host(nesle_batch* b, int kind, void* dst, std::size_t bytes) {
 int nesle_render(nesle_batch* b, std::uint32_t outputs) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
-        if (outputs == 0 || (outputs & ~7u) != 0) throw InvalidArgument("outputs must be a non-empty set of NESLE_FRAME_* bits");
+        const std::uint32_t frames = outputs & (NESLE_FRAME_RGB | NESLE_FRAME_PALETTE | NESLE_FRAME_GRAY84);
+        if (frames == 0 || (outputs & ~(frames | NESLE_FRAME_LIVE)) != 0)
+            throw InvalidArgument("outputs must be a non-empty set of NESLE_FRAME_* output bits, optionally with NESLE_FRAME_LIVE");
         if (b->ds.present == nullptr) throw InvalidArgument("frames are off for this batch (created with frames = 0)");
         b->activate();
         b->ensure_render_tables();
@@ -698,6 +707,16 @@ int nesle_render(nesle_batch* b, std::uint32_t outputs) {
         a.n = b->n();
         a.present = b->ds.present;
         a.present_stride = nesle::present::kHeader + b->ds.vram_stride;
+        if (outputs & NESLE_FRAME_LIVE) {
+            if (b->d_live_records == nullptr)
+                hip_check(hipMalloc(&b->d_live_records, static_cast<std::size_t>(a.n) * a.present_stride),
+                          "hipMalloc live records");
+            hip_check(nesle::launch_live_records(b->ds, b->d_live_records, b->stream), "record_kernel");
+            a.present = b->d_live_records;
+            a.cpu_rules = 1;
+            a.chr_ram = b->ds.chr_ram;
+            a.pitch = b->ds.pitch;
+        }
         a.chr = b->rom.chr.empty() ? nullptr : b->d_chr;
         a.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
         a.nt_mode = b->ds.nt_mode;

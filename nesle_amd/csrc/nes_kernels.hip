@@ -202,21 +202,25 @@ __global__ void __launch_bounds__(kBlock) seed_kernel(DeviceState s) {
     if (env < s.n) reward_seed(s, env, GlobalRam{s, env});
 }
 
-// Presentation snapshot from live state, so a render right after a reset or
-// state load is coherent (cuda_module.cu:1440-1463): one workgroup per
-// console (selected by mask, null = all) copies its video memory block.
-__global__ void __launch_bounds__(kBlock) seed_present_kernel(DeviceState s, const std::uint8_t* mask) {
+// Presentation records from live state: frame-start and frame-end
+// scroll/ctrl both the current ones, the mask and a copy of the video memory
+// block; one workgroup per console (selected by mask, null = all).  Into the
+// presentation snapshot (with the pre-render latch) after full resets and
+// state loads, so a render right after them is coherent (cuda_module.cu:
+// 1440-1463); or into a separate buffer for a render of live state.
+__global__ void __launch_bounds__(kBlock) record_kernel(DeviceState s, const std::uint8_t* mask, std::uint8_t* out,
+                                                        std::uint32_t latch) {
     const std::uint32_t env = blockIdx.x;
     if (mask != nullptr && mask[env] == 0) return;
     const std::uint32_t vs = s.vram_stride;
-    std::uint8_t* rec = s.present + static_cast<std::size_t>(env) * (present::kHeader + vs);
+    std::uint8_t* rec = out + static_cast<std::size_t>(env) * (present::kHeader + vs);
     const std::uint32_t t = threadIdx.x;
     if (t < present::kHeader) {
         const std::uint32_t sx = s.scroll_x[env], sy = s.scroll_y[env], ctrl = s.ctrl[env];
         const std::uint32_t k = t % 3;
         const std::uint32_t v = t == present::kMask ? s.mask[env] : t > present::kMask ? 0u : (k == 0 ? sx : k == 1 ? sy : ctrl);
         rec[t] = static_cast<std::uint8_t>(v);
-        if (t == 0) {
+        if (t == 0 && latch != 0) {
             s.lat_sx[env] = static_cast<std::uint8_t>(sx);
             s.lat_sy[env] = static_cast<std::uint8_t>(sy);
             s.lat_ctrl[env] = static_cast<std::uint8_t>(ctrl);
@@ -276,7 +280,13 @@ hipError_t launch_poke_ram_envs(const DeviceState& s, std::uint32_t addr, const 
 
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream) {
     if (s.n == 0 || s.present == nullptr) return hipSuccess;
-    seed_present_kernel<<<dim3(s.n), dim3(kBlock), 0, stream>>>(s, mask);
+    record_kernel<<<dim3(s.n), dim3(kBlock), 0, stream>>>(s, mask, s.present, 1u);
+    return hipGetLastError();
+}
+
+hipError_t launch_live_records(const DeviceState& s, std::uint8_t* out, hipStream_t stream) {
+    if (s.n == 0) return hipSuccess;
+    record_kernel<<<dim3(s.n), dim3(kBlock), 0, stream>>>(s, nullptr, out, 0u);
     return hipGetLastError();
 }
 

@@ -33,6 +33,9 @@ hipError_t launch_seed_baselines(const DeviceState& s, hipStream_t stream);
 hipError_t launch_zero_u64(unsigned long long* p, std::uint32_t n, hipStream_t stream);
 // Presentation snapshot (and pre-render latch) from live state, masked.
 hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, hipStream_t stream);
+// Records of every console's live state (present::kHeader + vram_stride bytes
+// each) into `out`, for a render of live state; the snapshot is untouched.
+hipError_t launch_live_records(const DeviceState& s, std::uint8_t* out, hipStream_t stream);
 
 // The calling thread's message for nesle_last_error(), from entry points
 // outside the batch (nes_host.hip keeps it).

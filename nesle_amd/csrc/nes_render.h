@@ -77,6 +77,13 @@ struct RenderArgs {
     std::uint8_t* palette;           // [n][240][256] or null
     std::uint8_t* rgb;               // [n][240][256][3] or null
     std::uint8_t* gray;              // [n][84][84] or null
+    // The reference CPU core's rules (ppu.hpp:213-545) instead of the
+    // batched core's: a background pixel is opaque when its pattern colour is
+    // non-zero (whatever its palette value), and CHR RAM is read.  Used with
+    // records of live state (start = end, so one scroll for the frame).
+    std::uint32_t cpu_rules;
+    const std::uint8_t* chr_ram;     // interleaved [8192][pitch] CHR RAM, or null
+    std::uint32_t pitch;
 };
 
 hipError_t launch_render(const RenderArgs& a, hipStream_t stream);

@@ -8,7 +8,11 @@
 // frame-start values), a background pixel whose palette value is 0 counts as
 // transparent, CHR RAM reads as 0, and the lowest-index sprite that is opaque
 // and not behind an opaque background pixel (of the frame-end view) wins.
-// RGB uses the renderer's 64-entry palette.  The gray observation is the
+// RGB uses the renderer's 64-entry palette.  A render of live state follows
+// the reference CPU core's renderer instead (ppu.hpp:213-545, what its
+// Console shows): records built from the current registers and video memory,
+// one scroll for the whole frame, a background pixel opaque whenever its
+// pattern colour is non-zero, and CHR RAM read.  The gray observation is the
 // pixel preprocessing of the reference's training project (project/
 // mario-rl-ram/src/mario_rl/wrappers.py:209-215): luma truncated to 8 bits,
 // then Pillow's BILINEAR resize to 84x84; the host computes its fixed-point
@@ -222,8 +226,20 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
         // 16 bytes (8 low-plane rows, 8 high-plane rows) become 8 row pairs.
         const std::uint32_t words = a.chr_size / 16;
         const uint4* c = reinterpret_cast<const uint4*>(a.chr);
+        // CHR RAM under the CPU core's rules: this console's bytes, gathered
+        // from the interleaved rows (byte `addr` of console env at addr * pitch + env).
+        const std::uint8_t* cram = (a.cpu_rules != 0 && words == 0) ? a.chr_ram : nullptr;
         for (std::uint32_t i = tid; i < 512; i += kThreads) {
-            const uint4 t = words != 0 ? c[i % words] : make_uint4(0, 0, 0, 0);
+            uint4 t = words != 0 ? c[i % words] : make_uint4(0, 0, 0, 0);
+            if (cram != nullptr) {
+                std::uint32_t w[4];
+                for (std::uint32_t q = 0; q < 4; ++q) {
+                    w[q] = 0;
+                    for (std::uint32_t j = 0; j < 4; ++j)
+                        w[q] |= static_cast<std::uint32_t>(cram[static_cast<std::size_t>(16 * i + 4 * q + j) * a.pitch + env]) << (8 * j);
+                }
+                t = make_uint4(w[0], w[1], w[2], w[3]);
+            }
             reinterpret_cast<uint4*>(chr)[i] = make_uint4(perm(t.z, t.x, 0x05010400u), perm(t.z, t.x, 0x07030602u),
                                                           perm(t.w, t.y, 0x05010400u), perm(t.w, t.y, 0x07030602u));
         }
@@ -247,9 +263,9 @@ __global__ void __launch_bounds__(kThreads) render_kernel(RenderArgs a) {
         std::uint32_t v = 0, g = 0, o = 0;
         for (std::uint32_t c = 0; c < 4; ++c) {
             std::uint32_t p;
-            if (tid < 4) {   // background: colour 0 and value 0 show the backdrop and are transparent
+            if (tid < 4) {   // background: colour 0 (and, batched rules, value 0) shows the backdrop, transparent
                 p = value(4 * q + c);
-                const bool opaque = c != 0 && p != 0;
+                const bool opaque = c != 0 && (p != 0 || a.cpu_rules != 0);
                 if (!opaque) p = value(0);
                 o |= (opaque ? 1u : 0u) << (8 * c);
             } else {

@@ -376,16 +376,27 @@ class _Gen:
         return None
 
     # -- whole ROM ---------------------------------------------------------
-    def build(self, seed: int, prg_banks: int = 2) -> SynthRom:
+    def build(self, seed: int, prg_banks: int = 2, split: bool = False) -> SynthRom:
         """``prg_banks`` 2: 32 KB PRG at $8000-$FFFF.  1: a 16 KB image (NROM-128),
         mirrored at $8000 and $C000: the program is assembled at $C000-$FFFF
         (RESET/main loop $C000-$CFFF, subroutines $D000-$EEFF) and the
         vectors point into the $8000 mirror, so the console starts, takes
-        NMIs and BRKs in the low copy and jumps or returns into the high one."""
+        NMIs and BRKs in the low copy and jumps or returns into the high one.
+
+        ``split``: the status-bar variant.  Sprite 0 sits at a seeded row near
+        the top of the screen, the NMI handler sets the status bar's scroll
+        (0, 0), and every pass of the main loop first waits for the sprite-0
+        flag of PPUSTATUS to clear (pre-render line) and set again (line 30),
+        burns a seeded, frame-dependent delay and then writes the play
+        field's scroll to $2005 (x from the x position, a seeded y), all
+        without IRQs; a shorter block of random work follows.  Frames then
+        start with the status-bar scroll and end with the play-field one."""
         a, r = self.a, self.r
         small = prg_banks == 1
         code_lo = 0xC000 if small else 0x8000
         main_stop = 0xCC00 if small else 0xB800   # the main loop's last block starts below this
+        if split:
+            main_stop = code_lo + 0x1000
         subs_at = 0xD000 if small else 0xC000
         done_init = r.range(25, 250)     # done fires after 8*done_init frames
         pointers = [r.range(0x0300, 0x0700) for _ in range(8)]
@@ -445,6 +456,19 @@ class _Gen:
 
         # Main loop fills the rest of the low code area.
         a.label("MAIN")
+        if split:
+            # Sprite-0 timed scroll split: PPUSTATUS bit 6 clears at the
+            # pre-render line and sets at line 30 (BIT copies it into V).
+            w0 = a.label()
+            a.op("BIT", "abs", 0x2002); a.op("BVS", "rel", w0)
+            w1 = a.label()
+            a.op("BIT", "abs", 0x2002); a.op("BVC", "rel", w1)
+            a.op("LDA", "zp", FRAME_COUNTER); a.op("AND", "imm", 0x1F)
+            a.op("CLC"); a.op("ADC", "imm", r.range(1, 64)); a.op("TAY")
+            dl = a.label()
+            a.op("DEY"); a.op("BNE", "rel", dl)
+            a.op("LDA", "zp", X_LO); a.op("STA", "abs", 0x2005)
+            a.op("LDA", "imm", r.range(0, 239)); a.op("STA", "abs", 0x2005)
         while a.pc < main_stop:
             self.emit_block(0, 12, None)
         a.op("JMP", "abs", "MAIN")
@@ -452,7 +476,9 @@ class _Gen:
             raise ValueError("main loop overflows into subroutines")
 
         # Data tables at $F000: palette, nametables, attributes, sprites, noise.
-        data = bytes(r.below(256) for _ in range(0x800))
+        data = bytearray(r.below(256) for _ in range(0x800))
+        if split:
+            data[0x400] = r.range(16, 40)   # sprite 0's top row - 1: the split lands at rows 25-49
         pal_bytes = bytes(b & 0x3F for b in data[:0x20])
         a.org(DATA_ADDR)
         a.byte(*pal_bytes)
@@ -499,7 +525,10 @@ class _Gen:
         a.op("LDA", "abs", 0x2007); a.op("STA", "zp", NMI_TEMP)
         # Scroll, control and mask.
         a.op("LDA", "abs", 0x2002)
-        a.op("LDA", "zp", X_LO); a.op("STA", "abs", 0x2005)
+        if split:   # the status bar's scroll: the frame starts with it
+            a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x2005)
+        else:
+            a.op("LDA", "zp", X_LO); a.op("STA", "abs", 0x2005)
         a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x2005)
         a.op("LDA", "imm", ctrl); a.op("STA", "abs", 0x2000)
         a.op("LDA", "imm", mask); a.op("STA", "abs", 0x2001)
@@ -524,9 +553,10 @@ class _Gen:
                         done_init=done_init, labels=dict(a.labels))
 
 
-def make_rom(seed: int, prg_banks: int = 2) -> SynthRom:
+def make_rom(seed: int, prg_banks: int = 2, split: bool = False) -> SynthRom:
     """The synthetic NROM image for ``seed`` (deterministic); ``prg_banks`` 1
-    gives the 16 KB (NROM-128) variant."""
+    gives the 16 KB (NROM-128) variant; ``split`` the status-bar variant
+    (sprite-0 timed mid-frame $2005 writes, see _Gen.build)."""
     if prg_banks not in (1, 2):
         raise ValueError("prg_banks must be 1 or 2")
-    return _Gen(seed).build(seed, prg_banks)
+    return _Gen(seed).build(seed, prg_banks, split)

@@ -77,3 +77,30 @@ def warm_snapshots(rom: bytes, warm_frames: list[int], seed: int) -> list[np.nda
         b.step()
     assert b.num_levels == n
     return [b.snapshot_export(s) for s in range(n)]
+
+
+_HIP = None
+
+
+def device_rows(b: abi.Batch, kind: int, rows, row_shape: tuple[int, ...]) -> dict[int, np.ndarray]:
+    """Selected rows of a device view, each copied alone (hipMemcpy of the HIP
+    runtime the batch runs on) -- for full-size batches whose whole view would
+    be gigabytes on the host."""
+    import ctypes
+
+    global _HIP
+    if _HIP is None:
+        abi.lib()                                    # torch first: one HIP runtime in the process
+        _HIP = ctypes.CDLL("libamdhip64.so.7")
+        _HIP.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        _HIP.hipMemcpy.restype = ctypes.c_int
+    b.synchronize()
+    v = b.view(kind)
+    row_bytes = int(np.prod(row_shape))
+    out = {}
+    for r in rows:
+        buf = np.empty(row_shape, dtype=np.uint8)
+        rc = _HIP.hipMemcpy(buf.ctypes.data, v.data + int(r) * row_bytes, row_bytes, 2)   # device to host
+        assert rc == 0, f"hipMemcpy failed ({rc})"
+        out[int(r)] = buf
+    return out

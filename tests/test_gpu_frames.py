@@ -14,7 +14,7 @@ import pytest
 
 from nesle_amd import abi, synthrom
 from oracle import oracle as O
-from tests.helpers import masks_for, say
+from tests.helpers import OracleBatch, device_rows, masks_for, say, warm_snapshots
 
 pytestmark = pytest.mark.gpu
 
@@ -259,3 +259,155 @@ def test_pixel_workload_full_size_sampled():
     for k in range(3):
         _step_all(b, oracles, 0x5EED, k, 4)
         _check(b, oracles, f"step {k}", abi.FRAME_GRAY84)
+
+
+def _record_matches(rec: np.ndarray, pres: np.ndarray, tag: str) -> None:
+    """A device presentation record (16-byte header, then palette, OAM and
+    nametable RAM) against the oracle's presentation state."""
+    P = O.PRESENT_OFF
+    np.testing.assert_array_equal(rec[0:7], pres[0:7], err_msg=f"{tag}: scroll/ctrl/mask")
+    np.testing.assert_array_equal(rec[16:48], pres[P["palette"]:P["palette"] + 32], err_msg=f"{tag}: palette")
+    np.testing.assert_array_equal(rec[48:304], pres[P["oam"]:P["oam"] + 256], err_msg=f"{tag}: OAM")
+    np.testing.assert_array_equal(rec[304:304 + 2048], pres[P["nametable"]:P["nametable"] + 2048],
+                                  err_msg=f"{tag}: nametables")
+
+
+def test_status_bar_rom_pixel_workload_full_size_with_auto_resets():
+    """The pixel workload on the status-bar ROM (sprite-0 timed mid-frame
+    $2005 writes, IRQ-free): 16,384 consoles, frame-skip 4, 4 snapshot levels
+    with short episodes, x-delta reward and auto-reset.  After every step,
+    sampled consoles' presentation records equal the oracle's (frames that
+    start with the status-bar scroll and end with the play-field scroll),
+    and so do their palette-value frames and 84x84 gray frames -- including
+    the frames of consoles restarted from a snapshot, whose first frame-start
+    scroll is the one latched before the reset."""
+    rom = synthrom.make_rom(2026, split=True).rom
+    snaps = warm_snapshots(rom, [33, 57, 90, 121], seed=303)
+    for i, s in enumerate(snaps):
+        s[O.OFF["ram"] + synthrom.DONE_BYTE] = 2 + i      # episodes of 9-32 frames from a snapshot
+    blobs = [bytes(s) for s in snaps]
+    n, steps = 16384, 16
+    rng = np.random.default_rng(305)
+    levels = rng.integers(0, 4, n).astype(np.uint8)
+    sample = sorted({0, 1, 63, 64, 255, 256, 8191, 8192, n - 1, *rng.integers(0, n, 7).tolist()})
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.01)
+    say(f"[gpu] status-bar pixel workload: N={n} fs=4 steps={steps} sample={sample}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.01)
+    b.set_snapshots(blobs, levels)
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        c.load(snaps[levels[e]])
+        c.seed_presentation()          # a full reset seeds the presentation records from live state
+    distinct = after_reset = ends = 0
+    restarted: set[int] = set()
+    for k in range(steps):
+        m = masks_for(404, n, k)
+        b.set_actions(m)
+        b.step(auto_reset=True)
+        _, rew, don = ob.step(m, 4)
+        np.testing.assert_array_equal(b.host(abi.VIEW_REWARDS)[sample], rew, err_msg=f"step {k} rewards")
+        np.testing.assert_array_equal(b.host(abi.VIEW_DONES)[sample], don, err_msg=f"step {k} dones")
+        b.render(abi.FRAME_PALETTE | abi.FRAME_GRAY84)
+        recs = device_rows(b, abi.VIEW_PRESENT, sample, (b.view(abi.VIEW_PRESENT).shape[1],))
+        pals = device_rows(b, abi.VIEW_FRAME_PALETTE, sample, (240, 256))
+        grays = device_rows(b, abi.VIEW_GRAY84, sample, (84, 84))
+        for j, e in enumerate(sample):
+            con = ob.cons[j]
+            _record_matches(recs[e], con.presentation(), f"step {k} env {e}")
+            want = con.render(snapshot=True)
+            bad = int((pals[e] != want).sum())
+            assert bad == 0, f"step {k} env {e}: {bad} palette values differ"
+            assert np.array_equal(grays[e], O.gray84(want)), f"step {k} env {e}: gray84"
+            distinct += tuple(recs[e][0:3]) != tuple(recs[e][3:6])
+            after_reset += j in restarted
+        restarted = set(np.nonzero(don)[0].tolist())
+        for j in restarted:
+            ob.cons[j].load(snaps[levels[sample[j]]])
+        ends += len(restarted)
+    say(f"[gpu]   {distinct} split frames, {ends} episode ends, {after_reset} frames right after a restart")
+    assert distinct >= steps * len(sample) // 2
+    assert ends >= len(sample) and after_reset >= len(sample) // 2
+
+
+def _h(a: np.ndarray) -> str:
+    return f"{O.fnv1a_np(np.ascontiguousarray(a)):016x}"
+
+
+@pytest.mark.parametrize("rom_seed", [1, 2, 3])
+def test_live_frames_match_the_reference_core_golden(rom_seed):
+    """One console over 600 frames (frame-skip 1, the single-env workload):
+    frames drawn from live state by the CPU core's rules (NESLE_FRAME_LIVE)
+    hash exactly as the reference nesle::Console's own RGB frames and their
+    84x84 gray observations (tests/golden/frames_rom{1,2,3}.json)."""
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).resolve().parent / "golden" / f"frames_rom{rom_seed}.json").read_text())
+    rom = synthrom.make_rom(rom_seed).rom
+    assert _h(np.frombuffer(rom, dtype=np.uint8)) == fx["rom_fnv1a"]
+    want = {r[0]: r for r in fx["records"]}
+    say(f"[gpu] live frames vs reference golden: rom{rom_seed} N=1 frames={max(want)}")
+    b = abi.Batch(rom, 1, frameskip=1)
+    checked = 0
+    for k in range(max(want)):
+        b.set_actions(masks_for(fx["action_seed"], 1, k))
+        b.step()
+        rec = want.get(k + 1)
+        if rec is None:
+            continue
+        b.render(abi.FRAME_RGB | abi.FRAME_GRAY84 | abi.FRAME_LIVE)
+        assert _h(b.host(abi.VIEW_FRAME_RGB)[0]) == rec[1], f"frame {k + 1}: RGB"
+        assert _h(b.host(abi.VIEW_GRAY84)[0]) == rec[2], f"frame {k + 1}: gray84"
+        checked += 1
+    assert checked == len(want)
+
+
+def test_live_frames_of_random_states_with_chr_ram():
+    """Live-state frames by the CPU core's rules on 64 consoles of a CHR RAM
+    cart, each loaded with its own random video memory, registers and CHR RAM
+    tiles: equal the oracle's CPU-rule frame of the same state (background
+    palette value 0 opaque, CHR RAM read, one scroll), and leave the
+    presentation snapshot as it was."""
+    rom = _rom(5, chr_ram=True)
+    n = 64
+    say(f"[gpu] live frames, random states, CHR RAM: N={n}")
+    b = abi.Batch(rom, n, frameskip=1)
+    base = O.Oracle(rom)
+    for k in range(15):
+        base.step(int(masks_for(8, 1, k)[0]), 1)
+    st0 = base.save()
+    rng = np.random.default_rng(4242)
+    oracles = {}
+    for e in range(n):
+        st = st0.copy()
+        st[O.OFF["oam"]:O.OFF["oam"] + 256] = rng.integers(0, 256, 256, dtype=np.uint8)
+        pal = rng.integers(0, 64, 32, dtype=np.uint8)
+        pal[rng.integers(0, 32, 8)] = 0
+        st[O.OFF["palette"]:O.OFF["palette"] + 32] = pal
+        st[O.OFF["nametable"]:O.OFF["nametable"] + 2048] = rng.integers(0, 256, 2048, dtype=np.uint8)
+        st[O.OFF["chr_ram"]:O.OFF["chr_ram"] + 8192] = rng.integers(0, 256, 8192, dtype=np.uint8)
+        st[O.OFF["ctrl"]] = rng.integers(0, 256)
+        st[O.OFF["mask"]] = 0x18 | rng.integers(0, 256) if e % 4 else rng.integers(0, 256)
+        st[O.OFF["scroll_x"]] = rng.integers(0, 256)
+        st[O.OFF["scroll_y"]] = rng.integers(0, 256)
+        mask = np.zeros(n, dtype=np.uint8)
+        mask[e] = 1
+        b.load_state(st, mask)
+        con = O.Oracle(rom)
+        con.load(st)
+        con.seed_presentation()
+        oracles[e] = con
+    before = b.host(abi.VIEW_PRESENT)
+    b.render(abi.FRAME_PALETTE | abi.FRAME_RGB | abi.FRAME_GRAY84 | abi.FRAME_LIVE)
+    pal, rgb, gray = b.host(abi.VIEW_FRAME_PALETTE), b.host(abi.VIEW_FRAME_RGB), b.host(abi.VIEW_GRAY84)
+    lut = O.palette_rgb()
+    for e, con in oracles.items():
+        want = con.render(snapshot=False, cpu_rules=True)
+        bad = int((pal[e] != want).sum())
+        assert bad == 0, f"env {e}: {bad} palette values differ"
+        assert np.array_equal(rgb[e], lut[want]) and np.array_equal(gray[e], O.gray84(want)), f"env {e}"
+    assert np.array_equal(b.host(abi.VIEW_PRESENT), before)
+    # The batched rules still draw the snapshot, with CHR RAM read as 0.
+    _check(b, oracles, "snapshot after a live render")
