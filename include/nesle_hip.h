@@ -123,6 +123,29 @@ void nesle_config_init(nesle_config* cfg);
  * reset_console 1227-1289).  num_envs must be 1..NESLE_MAX_ENVS. */
 int nesle_create(const nesle_config* cfg, const uint8_t* ines, size_t ines_len, nesle_batch** out);
 
+/* A batch without a cartridge: the reference's synthetic CudaBatch(num_envs,
+ * frameskip) (cuda_module.cu:368-379, name "cuda").  No console runs; every
+ * console's RAM holds the bytes the SMB reward rule reads (x position $006D/
+ * $0086, y viewport $00B5, lives $075A, player state $000E, BCD time
+ * $07F8-$07FA), powered on as cold_reset_synthetic_env does (batch_step.cuh:
+ * 244-260).  nesle_step and nesle_synthetic_step (below) move it; reward_kind
+ * is forced to the SMB rule, stats modes and snapshots are refused; frames
+ * render blank (power-on PPU state).  Views, resets and the RAM observation
+ * behave as for a console batch.  Fails like nesle_create for bad sizes. */
+int nesle_create_synthetic(const nesle_config* cfg, nesle_batch** out);
+
+/* One env-step of a synthetic batch.  apply_actions != 0 (the reference's
+ * step(), apply_actions_kernel + step_reward_kernel, cuda_module.cu:319-354,
+ * 546-565, kernels.cu:12-17): the pad moves x (Right +1, +1 more with B,
+ * Left -1, clamped to 0..$FFFF) and every max(1, 24 / frameskip)-th step of
+ * a console takes one from the BCD time, then the SMB rule scores it.
+ * apply_actions == 0 (the reference's step_device(), which launches only the
+ * reward kernel without a ROM, cuda_module.cu:620-633): the rule alone.
+ * auto_reset: consoles done after the step power on again (rewards and
+ * dones stay readable).  nesle_step on a synthetic batch is this call with
+ * apply_actions = 1.  Fails with NESLE_EINVAL on a console batch. */
+int nesle_synthetic_step(nesle_batch* b, int apply_actions, int auto_reset);
+
 /* Install a snapshot bank (FCEUX FCS or canonical NST1 blobs, detected by
  * magic) and the per-env level map (host, num_envs bytes; null = all 0), then
  * reset every console from it.  Replaces the 4- and 5-argument constructors

@@ -114,6 +114,8 @@ def lib():
     sig = {
         "nesle_config_init": (None, [ctypes.POINTER(Config)]),
         "nesle_create": (ctypes.c_int, [ctypes.POINTER(Config), ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(vp)]),
+        "nesle_create_synthetic": (ctypes.c_int, [ctypes.POINTER(Config), ctypes.POINTER(vp)]),
+        "nesle_synthetic_step": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int]),
         "nesle_set_snapshots": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_size_t),
                                                ctypes.c_uint32, _U8P]),
         "nesle_retain": (None, [vp]),
@@ -184,10 +186,11 @@ def parse_fcs(data: bytes) -> np.ndarray:
 class Batch:
     """Owning handle over one ``nesle_batch``."""
 
-    def __init__(self, rom: bytes, num_envs: int, frameskip: int = 4, *, reward_kind: int = REWARD_SMB,
+    def __init__(self, rom: bytes | None, num_envs: int, frameskip: int = 4, *, reward_kind: int = REWARD_SMB,
                  x_lo: int = 0x86, x_hi: int = 0x6D, done_addr: int = 0, clip: int = 15,
                  time_penalty: float = 0.0, max_instructions_per_frame: int = 0, device: int = -1,
                  frames: bool = True) -> None:
+        """``rom`` None: the ROM-less synthetic batch (nesle_create_synthetic)."""
         L = lib()
         cfg = Config()
         L.nesle_config_init(ctypes.byref(cfg))
@@ -198,7 +201,10 @@ class Batch:
         cfg.device = device
         cfg.frames = int(frames)
         h = ctypes.c_void_p()
-        _check(L.nesle_create(ctypes.byref(cfg), rom, len(rom), ctypes.byref(h)))
+        if rom is None:
+            _check(L.nesle_create_synthetic(ctypes.byref(cfg), ctypes.byref(h)))
+        else:
+            _check(L.nesle_create(ctypes.byref(cfg), rom, len(rom), ctypes.byref(h)))
         self.h = h
         self.n = num_envs
 
@@ -237,6 +243,9 @@ class Batch:
 
     def step(self, auto_reset: bool = False, stats_mode: int = 0) -> None:
         _check(lib().nesle_step(self.h, int(auto_reset), stats_mode))
+
+    def synthetic_step(self, apply_actions: bool = True, auto_reset: bool = False) -> None:
+        _check(lib().nesle_synthetic_step(self.h, int(apply_actions), int(auto_reset)))
 
     def census(self) -> dict:
         """The step kernel's census of the last stats-mode-3 step, by name."""

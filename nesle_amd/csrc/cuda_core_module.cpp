@@ -237,6 +237,20 @@ public:
         check(nesle_create(&cfg, bytes.data(), bytes.size(), &h_));
         n_ = num_envs;
     }
+    // The ROM-less synthetic batch, CudaBatch(num_envs, frameskip)
+    // (cuda_module.cu:368-379): name "cuda".
+    CudaBatch(std::uint32_t num_envs, std::uint32_t frameskip, std::int32_t device, bool frames) {
+        nesle_config cfg;
+        nesle_config_init(&cfg);
+        cfg.num_envs = num_envs;
+        cfg.frameskip = frameskip;
+        cfg.device = device;
+        cfg.frames = frames ? 1u : 0u;
+        frames_ = frames;
+        synthetic_ = true;
+        check(nesle_create_synthetic(&cfg, &h_));
+        n_ = num_envs;
+    }
     CudaBatch(const CudaBatch&) = delete;
     CudaBatch& operator=(const CudaBatch&) = delete;
     ~CudaBatch() { nesle_release(h_); }
@@ -325,7 +339,14 @@ public:
         int dtype = NESLE_DTYPE_U8;
         const auto ptr = device_actions(actions, n_, &dtype);
         check(nesle_set_actions(h_, reinterpret_cast<const void*>(ptr), dtype, 1));
-        check(nesle_step(h_, auto_reset ? 1 : 0, 0));
+        if (synthetic_) {
+            // Without a ROM the reference's step_device() runs the reward
+            // kernel alone: the actions are copied but move nothing
+            // (cuda_module.cu:620-633).
+            check(nesle_synthetic_step(h_, 0, auto_reset ? 1 : 0));
+        } else {
+            check(nesle_step(h_, auto_reset ? 1 : 0, 0));
+        }
         // The action copy, the step and the fused reset are ordered on the
         // batch's stream, so only an explicit request synchronises (the
         // reference also synchronises after every auto-reset step,
@@ -436,6 +457,7 @@ public:
     void set_stream(std::uintptr_t stream) { check(nesle_set_stream(h_, reinterpret_cast<void*>(stream))); }
 
     std::uint32_t num_envs() const { return n_; }
+    bool synthetic() const { return synthetic_; }
     std::uint32_t frameskip() const { return nesle_frameskip(h_); }
     std::uint32_t num_levels() const { return nesle_num_levels(h_); }
     bool has_snapshot() const { return has_snapshot_ && nesle_num_levels(h_) > 0; }
@@ -447,6 +469,7 @@ private:
     std::uint32_t n_ = 0;
     bool has_snapshot_ = false;
     bool frames_ = true;
+    bool synthetic_ = false;
 };
 
 RewardSpec reward_from_kwargs(const py::kwargs& kw) {
@@ -539,10 +562,8 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         py::arg("data"));
 
     py::class_<CudaBatch>(m, "CudaBatch")
-        .def(py::init([](std::uint32_t num_envs, std::uint32_t frameskip) -> CudaBatch* {
-                 (void)num_envs;
-                 (void)frameskip;
-                 throw py::value_error("the ROM-less synthetic batch is not provided by the HIP backend; pass rom_bytes");
+        .def(py::init([](std::uint32_t num_envs, std::uint32_t frameskip, const py::kwargs& kw) {
+                 return new CudaBatch(num_envs, frameskip, device_from_kwargs(kw), frames_from_kwargs(kw));
              }),
              py::arg("num_envs"), py::arg("frameskip"))
         .def(py::init([](std::uint32_t num_envs, std::uint32_t frameskip, const py::bytes& rom, const py::kwargs& kw) {
@@ -622,7 +643,7 @@ PYBIND11_MODULE(_cuda_core_native, m) {
         .def("kernel_timing", &CudaBatch::kernel_timing)
         .def("kernel_timing_split", &CudaBatch::kernel_timing_split)
         .def("set_stream", &CudaBatch::set_stream, py::arg("stream"))
-        .def_property_readonly("name", [](const CudaBatch&) { return std::string("cuda-console"); })
+        .def_property_readonly("name", [](const CudaBatch& b) { return std::string(b.synthetic() ? "cuda" : "cuda-console"); })
         .def_property_readonly("has_snapshot", &CudaBatch::has_snapshot)
         .def_property_readonly("frames", &CudaBatch::frames)
         .def_property_readonly("num_levels", &CudaBatch::num_levels)

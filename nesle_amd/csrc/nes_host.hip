@@ -205,6 +205,10 @@ std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a;
 
 struct nesle_batch {
     std::atomic<int> refs{1};
+    // The ROM-less synthetic batch (nesle_create_synthetic): no console runs;
+    // steps and resets are the synthetic kernels over RAM and the reward.
+    bool synthetic = false;
+    std::uint32_t* d_step_counts = nullptr;   // synthetic: env-steps per console
     int device = 0;
     hipStream_t stream = nullptr;
     nesle_config cfg{};
@@ -254,6 +258,7 @@ struct nesle_batch {
         (void)hipFree(d_frame_palette);
         (void)hipFree(d_gray84);
         (void)hipFree(d_live_records);
+        (void)hipFree(d_step_counts);
         (void)hipFree(d_render_tables);
     }
 
@@ -442,48 +447,100 @@ int nesle_parse_fcs(const std::uint8_t* bytes, std::size_t len, std::uint8_t* ou
     });
 }
 
+namespace {
+
+void check_config(const nesle_config* cfg) {
+    if (cfg->num_envs == 0) throw InvalidArgument("num_envs must be positive");
+    if (cfg->num_envs > NESLE_MAX_ENVS)
+        throw InvalidArgument("num_envs must be at most " + std::to_string(NESLE_MAX_ENVS));
+    if (cfg->frameskip == 0) throw InvalidArgument("frameskip must be positive");
+    if (cfg->reward_kind > NESLE_REWARD_XDELTA) throw InvalidArgument("unknown reward_kind");
+}
+
+// Allocate and power on a batch for `b->rom` (parsed and checked by the caller).
+void open_batch(nesle_batch* b, const nesle_config* cfg) {
+    int dev = cfg->device;
+    if (dev < 0) hip_check(hipGetDevice(&dev), "hipGetDevice");
+    b->device = dev;
+    b->activate();
+    b->pitch = static_cast<std::uint32_t>(align_up(cfg->num_envs, 256));
+    DeviceState& s = b->ds;
+    s.n = cfg->num_envs;
+    s.pitch = b->pitch;
+    s.nt_mode = b->rom.info.nametable_arrangement;
+    s.nt_bytes = s.nt_mode == 2 ? 4096u : 2048u;
+    s.vram_stride = nesle::vram::stride(s.nt_bytes);
+    s.prg_mask = static_cast<std::uint32_t>(b->rom.prg.size() - 1);
+    s.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
+    s.reward_kind = b->cfg.reward_kind;
+    s.x_lo = b->cfg.x_lo & 0x7FF;
+    s.x_hi = b->cfg.x_hi & 0x7FF;
+    s.done_addr = b->cfg.done_addr & 0x7FF;
+    s.clip = b->cfg.clip;
+    s.time_penalty = b->cfg.time_penalty;
+    b->allocate();
+    b->host_to_device(b->d_prg, b->rom.prg.data(), b->rom.prg.size(), "upload PRG ROM");
+    if (!b->rom.chr.empty()) b->host_to_device(b->d_chr, b->rom.chr.data(), b->rom.chr.size(), "upload CHR ROM");
+    hip_check(nesle::launch_reset(s, nullptr, b->stream), "reset_kernel");
+    if (b->synthetic) {
+        hip_check(hipMalloc(&b->d_step_counts, sizeof(std::uint32_t) * s.n), "hipMalloc step counts");
+        hip_check(nesle::launch_synthetic_reset(s, nullptr, b->d_step_counts, b->stream), "synthetic_reset_kernel");
+    }
+    b->seed_present(nullptr);
+    b->refresh_obs();
+    b->sync();
+}
+
+}  // namespace
+
 int nesle_create(const nesle_config* cfg, const std::uint8_t* ines, std::size_t ines_len, nesle_batch** out) {
     return guarded([&] {
         if (out == nullptr || cfg == nullptr) throw InvalidArgument("null argument");
         *out = nullptr;
-        if (cfg->num_envs == 0) throw InvalidArgument("num_envs must be positive");
-        if (cfg->num_envs > NESLE_MAX_ENVS)
-            throw InvalidArgument("num_envs must be at most " + std::to_string(NESLE_MAX_ENVS));
-        if (cfg->frameskip == 0) throw InvalidArgument("frameskip must be positive");
-        if (cfg->reward_kind > NESLE_REWARD_XDELTA) throw InvalidArgument("unknown reward_kind");
+        check_config(cfg);
         auto b = std::make_unique<nesle_batch>();
         b->cfg = *cfg;
         if (b->cfg.max_instructions_per_frame == 0) b->cfg.max_instructions_per_frame = 200000;
         b->rom = parse_ines(ines, ines_len);
         if (b->rom.info.mapper != 0 || (b->rom.prg.size() != 16384 && b->rom.prg.size() != 32768))
             throw InvalidArgument("only mapper 0 (NROM) cartridges run on this console");
-        int dev = cfg->device;
-        if (dev < 0) hip_check(hipGetDevice(&dev), "hipGetDevice");
-        b->device = dev;
-        b->activate();
-        b->pitch = static_cast<std::uint32_t>(align_up(cfg->num_envs, 256));
-        DeviceState& s = b->ds;
-        s.n = cfg->num_envs;
-        s.pitch = b->pitch;
-        s.nt_mode = b->rom.info.nametable_arrangement;
-        s.nt_bytes = s.nt_mode == 2 ? 4096u : 2048u;
-        s.vram_stride = nesle::vram::stride(s.nt_bytes);
-        s.prg_mask = static_cast<std::uint32_t>(b->rom.prg.size() - 1);
-        s.chr_size = static_cast<std::uint32_t>(b->rom.chr.size());
-        s.reward_kind = b->cfg.reward_kind;
-        s.x_lo = b->cfg.x_lo & 0x7FF;
-        s.x_hi = b->cfg.x_hi & 0x7FF;
-        s.done_addr = b->cfg.done_addr & 0x7FF;
-        s.clip = b->cfg.clip;
-        s.time_penalty = b->cfg.time_penalty;
-        b->allocate();
-        b->host_to_device(b->d_prg, b->rom.prg.data(), b->rom.prg.size(), "upload PRG ROM");
-        if (!b->rom.chr.empty()) b->host_to_device(b->d_chr, b->rom.chr.data(), b->rom.chr.size(), "upload CHR ROM");
-        hip_check(nesle::launch_reset(s, nullptr, b->stream), "reset_kernel");
-        b->seed_present(nullptr);
-        b->refresh_obs();
-        b->sync();
+        open_batch(b.get(), cfg);
         *out = b.release();
+    });
+}
+
+int nesle_create_synthetic(const nesle_config* cfg, nesle_batch** out) {
+    return guarded([&] {
+        if (out == nullptr || cfg == nullptr) throw InvalidArgument("null argument");
+        *out = nullptr;
+        check_config(cfg);
+        auto b = std::make_unique<nesle_batch>();
+        b->cfg = *cfg;
+        b->cfg.reward_kind = NESLE_REWARD_SMB;   // the synthetic RAM is scored by the SMB rule only
+        if (b->cfg.max_instructions_per_frame == 0) b->cfg.max_instructions_per_frame = 200000;
+        b->synthetic = true;
+        // No cartridge: an all-zero NROM-128 image stands in, so the batch's
+        // memory map, views and (blank) frames exist; no console ever runs it.
+        b->rom.info.prg_rom_size = 16384;
+        b->rom.info.chr_rom_size = 8192;
+        b->rom.prg.assign(16384, 0);
+        b->rom.chr.assign(8192, 0);
+        open_batch(b.get(), &b->cfg);
+        *out = b.release();
+    });
+}
+
+int nesle_synthetic_step(nesle_batch* b, int apply_actions, int auto_reset) {
+    return guarded([&] {
+        if (b == nullptr) throw InvalidArgument("null batch");
+        if (!b->synthetic) throw InvalidArgument("nesle_synthetic_step needs a batch from nesle_create_synthetic");
+        b->activate();
+        hip_check(nesle::launch_synthetic_step(b->ds, b->cfg.frameskip, b->d_step_counts, apply_actions != 0, b->stream),
+                  "synthetic_step_kernel");
+        if (auto_reset != 0)
+            hip_check(nesle::launch_synthetic_reset(b->ds, b->ds.done, b->d_step_counts, b->stream),
+                      "synthetic_reset_kernel");
+        b->refresh_obs();
     });
 }
 
@@ -491,6 +548,7 @@ int nesle_set_snapshots(nesle_batch* b, const std::uint8_t* const* blobs, const 
                         const std::uint8_t* env_to_level) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
+        if (b->synthetic) throw InvalidArgument("the ROM-less synthetic batch takes no snapshots");
         if (count == 0) throw InvalidArgument("the snapshot list is empty: give at least one snapshot");
         if (count > 255) throw InvalidArgument("a batch holds at most 255 snapshot levels");
         std::vector<std::uint8_t> host(static_cast<std::size_t>(count) * blob::kBytes);
@@ -536,7 +594,10 @@ int nesle_reset(nesle_batch* b) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
         b->activate();
-        hip_check(nesle::launch_reset(b->ds, nullptr, b->stream), "reset_kernel");
+        if (b->synthetic)
+            hip_check(nesle::launch_synthetic_reset(b->ds, nullptr, b->d_step_counts, b->stream), "synthetic_reset_kernel");
+        else
+            hip_check(nesle::launch_reset(b->ds, nullptr, b->stream), "reset_kernel");
         b->seed_present(nullptr);
         b->refresh_obs();
         b->sync();
@@ -552,7 +613,10 @@ int nesle_reset_envs(nesle_batch* b, const std::uint8_t* mask, int mask_on_devic
             b->host_to_device(b->d_mask, mask, b->n(), "copy reset mask");
             dmask = b->d_mask;
         }
-        hip_check(nesle::launch_reset(b->ds, dmask, b->stream), "reset_kernel");
+        if (b->synthetic)
+            hip_check(nesle::launch_synthetic_reset(b->ds, dmask, b->d_step_counts, b->stream), "synthetic_reset_kernel");
+        else
+            hip_check(nesle::launch_reset(b->ds, dmask, b->stream), "reset_kernel");
         b->refresh_obs();
         if (!mask_on_device) b->sync();   // a device mask stays ordered on the stream
     });
@@ -590,6 +654,17 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
         if (stats_mode < 0 || stats_mode > 3) throw InvalidArgument("stats_mode must be 0, 1, 2 or 3");
+        if (b->synthetic) {   // no console runs: no instruction statistics (cuda_module.cu:669-671)
+            if (stats_mode != 0) throw std::runtime_error("step statistics need a console batch (one made from a ROM)");
+            b->activate();
+            hip_check(nesle::launch_synthetic_step(b->ds, b->cfg.frameskip, b->d_step_counts, true, b->stream),
+                      "synthetic_step_kernel");
+            if (auto_reset != 0)
+                hip_check(nesle::launch_synthetic_reset(b->ds, b->ds.done, b->d_step_counts, b->stream),
+                          "synthetic_reset_kernel");
+            b->refresh_obs();
+            return;
+        }
         b->activate();
         if (stats_mode != 0) {
             b->ensure_stats();
@@ -742,6 +817,7 @@ int nesle_save_state(nesle_batch* b, std::uint32_t env, std::uint8_t* out_blob) 
 int nesle_load_state(nesle_batch* b, const std::uint8_t* data, std::size_t len, const std::uint8_t* mask) {
     return guarded([&] {
         if (b == nullptr || data == nullptr) throw InvalidArgument("null argument");
+        if (b->synthetic) throw InvalidArgument("the ROM-less synthetic batch has no console state to load");
         b->activate();
         const auto c = to_canonical(data, len);
         b->host_to_device(b->d_blob, c.data(), c.size(), "upload state");
@@ -760,6 +836,7 @@ int nesle_load_state(nesle_batch* b, const std::uint8_t* data, std::size_t len, 
 int nesle_snapshot_capture(nesle_batch* b, std::uint32_t env, std::uint32_t slot) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
+        if (b->synthetic) throw InvalidArgument("the ROM-less synthetic batch takes no snapshots");
         if (env >= b->n()) throw InvalidArgument("env out of range");
         if (slot > b->num_levels) throw InvalidArgument("slot must be an existing level or the next free one");
         b->activate();

@@ -233,7 +233,95 @@ __global__ void __launch_bounds__(kBlock) record_kernel(DeviceState s, const std
 
 inline std::uint32_t blocks_for(std::uint32_t n) { return (n + kBlock - 1) / kBlock; }
 
+// ---- the ROM-less synthetic batch (CudaBatch(num_envs, frameskip)) ----------
+// Not a console: RAM holds only the bytes the SMB reward rule reads, moved
+// by the pad (cpp/bindings/cuda_module.cu:319-354) and scored by that rule
+// (cpp/src/cuda/kernels.cu:12-17).  One thread per console, RAM rows
+// interleaved as everywhere else (row * pitch + env, coalesced over a wave).
+constexpr std::uint32_t kSynthXPage = 0x6D, kSynthXScreen = 0x86, kSynthYViewport = 0xB5, kSynthLives = 0x75A;
+constexpr std::uint32_t kSynthState = 0x0E, kSynthTime = 0x7F8;
+
+// Power-on of the synthetic console (batch_step.cuh:244-260): RAM cleared,
+// then x = $0102, y viewport 1, 2 lives, time 400; reward baselines to match.
+// A full reset (mask null) also clears rewards, dones and step counts, as the
+// reference's reset() does (cuda_module.cu:469-512); a masked reset leaves
+// the step's rewards and dones readable (they are the last_* values).
+__global__ void __launch_bounds__(kBlock) synthetic_reset_kernel(DeviceState s, const std::uint8_t* mask,
+                                                                 std::uint32_t* step_counts) {
+    const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
+    if (env >= s.n || (mask != nullptr && mask[env] == 0)) return;
+    std::uint8_t* ram = s.ram + env;
+    const std::size_t P = s.pitch;
+    for (std::uint32_t a = 0; a < kRamBytes; ++a) ram[a * P] = 0;
+    ram[kSynthXPage * P] = 1;
+    ram[kSynthXScreen * P] = 2;
+    ram[kSynthYViewport * P] = 1;
+    ram[kSynthLives * P] = 2;
+    ram[kSynthTime * P] = 4;   // BCD digits 4, 0, 0
+    s.prev_x[env] = 0x102;
+    s.prev_time[env] = 400;
+    if (mask == nullptr) {
+        s.rewards[env] = 0.0f;
+        s.done[env] = 0;
+        step_counts[env] = 0;
+    }
+}
+
+// One env-step.  With `apply_actions` (the reference's step()) the pad moves
+// x first -- Right +1, +1 more with B, Left -1, clamped to 0..$FFFF -- and
+// every max(1, 24 / frameskip)-th step of the console (from its first)
+// takes one from the 3-digit BCD time (not below 0); then the SMB rule
+// scores the RAM against the baselines.  step_device() runs the rule alone
+// (cuda_module.cu:620-633 launches only the reward kernel without a ROM).
+__global__ void __launch_bounds__(kBlock) synthetic_step_kernel(DeviceState s, std::uint32_t frameskip,
+                                                                std::uint32_t* step_counts,
+                                                                std::uint32_t apply_actions) {
+    const std::uint32_t env = blockIdx.x * kBlock + threadIdx.x;
+    if (env >= s.n) return;
+    std::uint8_t* ram = s.ram + env;
+    const std::size_t P = s.pitch;
+    if (apply_actions != 0) {
+        const std::uint32_t pad = s.actions[env];
+        std::int32_t dx = (pad & 0x80) ? 1 + ((pad & 0x02) ? 1 : 0) : 0;
+        dx -= (pad & 0x40) ? 1 : 0;
+        std::int32_t x = static_cast<std::int32_t>(ram[kSynthXPage * P]) * 256 + ram[kSynthXScreen * P] + dx;
+        x = x < 0 ? 0 : (x > 0xFFFF ? 0xFFFF : x);
+        ram[kSynthXPage * P] = static_cast<std::uint8_t>(x >> 8);
+        ram[kSynthXScreen * P] = static_cast<std::uint8_t>(x);
+        const std::uint32_t fs = frameskip == 0 ? 1u : frameskip;
+        const std::uint32_t cadence = 24u / fs == 0 ? 1u : 24u / fs;
+        const std::uint32_t k = step_counts[env];
+        step_counts[env] = k + 1;
+        if (k % cadence == 0) {
+            std::int32_t t = (ram[kSynthTime * P] & 15) * 100 + (ram[(kSynthTime + 1) * P] & 15) * 10 +
+                             (ram[(kSynthTime + 2) * P] & 15);
+            t = t > 0 ? t - 1 : 0;
+            ram[kSynthTime * P] = static_cast<std::uint8_t>(t / 100);
+            ram[(kSynthTime + 1) * P] = static_cast<std::uint8_t>((t / 10) % 10);
+            ram[(kSynthTime + 2) * P] = static_cast<std::uint8_t>(t % 10);
+        }
+    }
+    float reward = 0.0f;
+    std::uint32_t done = 0;
+    reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
+    s.rewards[env] = reward;
+    s.done[env] = static_cast<std::uint8_t>(done);
+}
+
 }  // namespace
+
+hipError_t launch_synthetic_reset(const DeviceState& s, const std::uint8_t* mask, std::uint32_t* step_counts,
+                                  hipStream_t stream) {
+    synthetic_reset_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, mask, step_counts);
+    return hipGetLastError();
+}
+
+hipError_t launch_synthetic_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t* step_counts,
+                                 bool apply_actions, hipStream_t stream) {
+    synthetic_step_kernel<<<dim3(blocks_for(s.n)), dim3(kBlock), 0, stream>>>(s, frameskip, step_counts,
+                                                                                apply_actions ? 1u : 0u);
+    return hipGetLastError();
+}
 
 hipError_t launch_restore(const DeviceState& s, const std::uint8_t* mask, const std::uint8_t* fixed_blob,
                           hipStream_t stream) {

@@ -37,6 +37,14 @@ hipError_t launch_seed_present(const DeviceState& s, const std::uint8_t* mask, h
 // each) into `out`, for a render of live state; the snapshot is untouched.
 hipError_t launch_live_records(const DeviceState& s, std::uint8_t* out, hipStream_t stream);
 
+// The ROM-less synthetic batch: masked (null = all, which also clears
+// rewards, dones and step counts) power-on, and one env-step (pad applied
+// or not) scored by the SMB rule.
+hipError_t launch_synthetic_reset(const DeviceState& s, const std::uint8_t* mask, std::uint32_t* step_counts,
+                                  hipStream_t stream);
+hipError_t launch_synthetic_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t* step_counts,
+                                 bool apply_actions, hipStream_t stream);
+
 // The calling thread's message for nesle_last_error(), from entry points
 // outside the batch (nes_host.hip keeps it).
 void set_last_error(const std::string& msg);
