@@ -62,6 +62,41 @@ int nesle_ppo_head_static(const float* logits, const float* value, const int64_t
                           double clip_coef, double ent_coef, double vf_coef, float* dlogits, float* dvalue,
                           float* loss, float* clipfrac, float* accum, void* stream);
 
+/* ---- the shaped Super Mario Bros. reward of the trainer ----------------------
+ * The reference trainer's reward_mode="smart" (src/nesle/native_ppo.py:120-316,
+ * TorchSmartMarioReward): progress, checkpoints, score, kills, coins, finish
+ * zone, flag, stalling, button, death and time terms from the env-step's RAM,
+ * pad masks and done flags, one thread per console, float32 rounded as
+ * PyTorch rounds it (bit-identical to the reference's tensor arithmetic).
+ * Device pointers, work on the caller's stream; nothing allocated, nothing
+ * synchronised (capturable in a graph). */
+
+/* 32-bit words of tracking state per console ([11][n], row-major). */
+#define NESLE_SMB_SHAPED_STATE_WORDS 11u
+
+/* The reward's constants (TorchSmartMarioReward's class attributes). */
+typedef struct nesle_smb_shaped_params {
+    float progress_scale, backtrack_scale, checkpoint_bonus, checkpoint_width, score_scale, coin_bonus, kill_bonus;
+    float finish_zone_x, finish_zone_bonus, flag_zone_x, flag_bonus, death_penalty, time_penalty;
+    float stall_penalty, max_stall_penalty, jump_penalty, neutral_jump_penalty, repeated_jump_penalty;
+    float max_repeated_jump_penalty, left_penalty, bad_button_penalty;
+    int32_t stall_window, repeated_jump_window;
+} nesle_smb_shaped_params;
+
+/* The reference's values (native_ppo.py:135-157). */
+void nesle_smb_shaped_defaults(nesle_smb_shaped_params* params);
+
+/* Start episodes: the tracking state of consoles with mask[e] != 0 (mask
+ * null = all) from their RAM (ram: [n][2048] env-major).  Replaces
+ * reset/reset_where (native_ppo.py:171-207). */
+int nesle_smb_shaped_reset(const uint8_t* ram, const uint8_t* mask, uint32_t n, void* state, void* stream);
+
+/* Reward of one env-step into reward[n] from the step's RAM (before any
+ * reset), pad masks and done flags (uint8 [n] each); updates the state.
+ * Replaces compute (native_ppo.py:209-278). */
+int nesle_smb_shaped_reward(const uint8_t* ram, const uint8_t* pads, const uint8_t* dones, uint32_t n,
+                            const nesle_smb_shaped_params* params, void* state, float* reward, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,7 @@ VIEW_INSTRUCTIONS, VIEW_FRAMES, VIEW_BUDGET_HITS, VIEW_OPCODES, VIEW_PCS, VIEW_O
 VIEW_FRAME_RGB, VIEW_FRAME_PALETTE, VIEW_GRAY84 = 10, 11, 12
 VIEW_CENSUS = 13
 VIEW_PRESENT = 14   # presentation records [n][16 + video memory block]
+SHAPED_STATE_WORDS = 11   # NESLE_SMB_SHAPED_STATE_WORDS
 # Step-kernel census slots (nesle_amd/csrc/nes_layout.h, namespace census).
 CENSUS_FIELDS = ("waves", "iterations", "rare", "rare_io_write", "rare_side", "rare_idle", "rare_illegal",
                  "rare_timing", "rare_budget", "rare_outside", "rare_only_io_write", "dma", "present", "io_read",
@@ -66,6 +67,17 @@ class View(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("device_id", ctypes.c_int32),
     ]
+
+
+class ShapedParams(ctypes.Structure):
+    """nesle_smb_shaped_params (include/nesle_ppo.h)."""
+    FLOATS = ("progress_scale", "backtrack_scale", "checkpoint_bonus", "checkpoint_width", "score_scale",
+              "coin_bonus", "kill_bonus", "finish_zone_x", "finish_zone_bonus", "flag_zone_x", "flag_bonus",
+              "death_penalty", "time_penalty", "stall_penalty", "max_stall_penalty", "jump_penalty",
+              "neutral_jump_penalty", "repeated_jump_penalty", "max_repeated_jump_penalty", "left_penalty",
+              "bad_button_penalty")
+    _fields_ = [(name, ctypes.c_float) for name in FLOATS] + [("stall_window", ctypes.c_int32),
+                                                              ("repeated_jump_window", ctypes.c_int32)]
 
 
 class RomInfo(ctypes.Structure):
@@ -153,6 +165,10 @@ def lib():
         "nesle_ppo_head_static": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32,
                                                  ctypes.c_double, ctypes.c_double, ctypes.c_double, vp, vp, vp, vp,
                                                  vp, vp]),
+        "nesle_smb_shaped_defaults": (None, [ctypes.POINTER(ShapedParams)]),
+        "nesle_smb_shaped_reset": (ctypes.c_int, [vp, vp, ctypes.c_uint32, vp, vp]),
+        "nesle_smb_shaped_reward": (ctypes.c_int, [vp, vp, vp, ctypes.c_uint32, ctypes.POINTER(ShapedParams), vp,
+                                                   vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

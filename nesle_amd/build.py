@@ -27,7 +27,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnesle_hip.so"
 HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_kernels.hip", CSRC / "nes_render.hip", CSRC / "nes_host.hip",
-               CSRC / "ppo_head.hip"]
+               CSRC / "ppo_head.hip", CSRC / "smb_shaped.hip"]
 SHIM_SOURCE = CSRC / "cuda_core_module.cpp"
 
 HIP_FLAGS = [

@@ -29,6 +29,7 @@ the batch's stream), whose share of the wall time is the emulator share.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import math
 import time
 from dataclasses import asdict, dataclass, field
@@ -61,12 +62,17 @@ class NativePPOConfig:
     vf_coef: float = 0.5
     max_grad_norm: float = 0.5
     hidden_size: int = 256
-    # "minimal": the batch's in-kernel reward rule.  The reference's shaped
-    # SMB reward ("smart") is not part of this build and is refused.
+    # "minimal": the batch's in-kernel reward rule; "smart": the reference's
+    # shaped SMB reward (SmartMarioReward, a HIP kernel over the step's RAM).
     reward_mode: str = "minimal"
+    # Smart-reward overrides (None keeps the reward's defaults).
+    flag_bonus: float | None = None
+    finish_zone_bonus: float | None = None
+    death_penalty: float | None = None
     seed: int = 1
     checkpoint_path: str = "nesle_native_ppo.pt"
     log_interval: int = 1
+    progress_bar: bool = False
     # Additions: weight init ("orthogonal" as the reference trainer, or
     # "xavier"), the in-kernel reward rule (CudaBatch ``reward=`` spec; None =
     # the SMB rule), whether to write checkpoints, and whether rollouts after
@@ -147,6 +153,85 @@ def _explained_variance(values, returns) -> float:
     with torch.no_grad():
         var_ret, var_err = torch.stack((returns, returns - values)).var(dim=1).tolist()
     return float("nan") if var_ret == 0.0 else 1.0 - var_err / var_ret
+
+
+# ---- shaped reward ---------------------------------------------------------
+
+def smart_reward_params(config: NativePPOConfig):
+    """The shaped reward's constants (the reference's TorchSmartMarioReward
+    values, native_ppo.py:135-157) with the config's overrides
+    (native_ppo.py:424-432)."""
+    from nesle_amd import abi
+
+    params = abi.ShapedParams()
+    abi.lib().nesle_smb_shaped_defaults(ctypes.byref(params))
+    for name in ("flag_bonus", "finish_zone_bonus", "death_penalty"):
+        value = getattr(config, name)
+        if value is not None:
+            setattr(params, name, float(value))
+    return params
+
+
+class SmartMarioReward:
+    """The reference trainer's shaped Super Mario Bros. reward
+    (TorchSmartMarioReward, native_ppo.py:120-316) as one HIP kernel per call
+    (``nesle_smb_shaped_reward``, include/nesle_ppo.h): progress, checkpoints,
+    score, kills, coins, finish zone, flag, stalling, button, death and time
+    terms, bit-identical to the reference's float32 tensor arithmetic.  The
+    tracking state is an [11, N] int32 device tensor; every call is enqueued
+    on the current stream, allocates nothing and reads nothing back, so a
+    rollout graph can hold it."""
+
+    def __init__(self, num_envs: int, config: NativePPOConfig | None = None, device=None) -> None:
+        torch, _, _ = _require_torch()
+        from nesle_amd import abi
+
+        self.n = int(num_envs)
+        self.params = smart_reward_params(config or NativePPOConfig(""))
+        dev = device if device is not None else torch.device("cuda")
+        self.state = torch.zeros((abi.SHAPED_STATE_WORDS, self.n), dtype=torch.int32, device=dev)
+        self.out = torch.zeros(self.n, dtype=torch.float32, device=dev)
+        self._lib = abi.lib()
+        self._check = abi._check
+
+    def _checked(self, t, dtype, what: str):
+        torch, _, _ = _require_torch()
+        if not t.is_cuda or t.dtype != dtype or not t.is_contiguous() or t.shape[0] != self.n:
+            raise ValueError(f"SmartMarioReward: {what} must be a contiguous {dtype} GPU tensor with "
+                             f"{self.n} rows, got {tuple(t.shape)} {t.dtype} on {t.device}")
+        return t
+
+    def reset(self, ram) -> None:
+        self.reset_where(None, ram)
+
+    def reset_where(self, mask, ram) -> None:
+        """Start episodes of the consoles in ``mask`` (bool/uint8 [N]; None =
+        all) from ``ram`` ([N, 2048] uint8)."""
+        torch, _, _ = _require_torch()
+        self._checked(ram, torch.uint8, "ram")
+        m = None
+        if mask is not None:
+            m = self._checked(mask.to(torch.uint8) if mask.dtype != torch.uint8 else mask, torch.uint8, "mask")
+            self._mask_keep = m    # keep the converted mask alive until the kernel is enqueued
+        stream = torch.cuda.current_stream().cuda_stream
+        self._check(self._lib.nesle_smb_shaped_reset(ram.data_ptr(), None if m is None else m.data_ptr(), self.n,
+                                                     self.state.data_ptr(), stream))
+
+    def compute(self, ram, action_masks, done):
+        """Reward of the step that produced ``ram`` (before any reset) from
+        the step's pad masks and done flags; updates the tracking state.
+        Returns a float32 [N] tensor that the next call overwrites."""
+        torch, _, _ = _require_torch()
+        self._checked(ram, torch.uint8, "ram")
+        pads = self._checked(action_masks, torch.uint8, "action_masks")
+        d = done.to(torch.uint8) if done.dtype != torch.uint8 else done
+        self._checked(d, torch.uint8, "done")
+        self._done_keep = d
+        stream = torch.cuda.current_stream().cuda_stream
+        self._check(self._lib.nesle_smb_shaped_reward(ram.data_ptr(), pads.data_ptr(), d.data_ptr(), self.n,
+                                                      ctypes.byref(self.params), self.state.data_ptr(),
+                                                      self.out.data_ptr(), stream))
+        return self.out
 
 
 # ---- checkpoints -----------------------------------------------------------
@@ -452,9 +537,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         raise ValueError(
             f"rollout produces {rollout_timesteps} samples per update (num_envs={config.num_envs} * "
             f"n_steps={config.n_steps}) but batch_size={config.batch_size} is larger")
-    if config.reward_mode != "minimal":
-        raise ValueError(f"reward_mode {config.reward_mode!r} is not available: this build trains on the "
-                         "batch's in-kernel reward rule only (reward_mode='minimal', rule chosen by `reward`)")
+    if config.reward_mode not in ("minimal", "smart"):
+        raise ValueError(f"unknown reward_mode {config.reward_mode!r} (expected 'minimal' or 'smart')")
     torch, _, _ = _require_torch()
     if not torch.cuda.is_available():
         raise SystemExit("native PPO needs a GPU")
@@ -487,6 +571,14 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     ram = from_dlpack(batch.ram_device())          # [N, 2048] uint8, refreshed by every step
     rewards_view = from_dlpack(batch.rewards_device())
     dones_view = from_dlpack(batch.last_done_device())
+    # The shaped reward reads the step's RAM before any reset, so with it the
+    # step runs without auto-reset and done consoles are reset afterwards
+    # through a device mask (the reference's order, native_ppo.py:486-509,
+    # without its host reads).
+    rewarder = None
+    if config.reward_mode == "smart":
+        rewarder = SmartMarioReward(config.num_envs, config, dev)
+        rewarder.reset(ram)
 
     T = config.n_steps
     obs_buf = torch.empty((T, n, obs_dim), dtype=torch.uint8, device=dev)
@@ -521,14 +613,22 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
         actions_buf[t].copy_(action)
         values_buf[t].copy_(value)
         pad = mask_table[action]
-        batch.step_device(pad, auto_reset=True, synchronize=False)
+        batch.step_device(pad, auto_reset=rewarder is None, synchronize=False)
         done = dones_view.bool()
         episode_lengths.add_(1.0)
-        reward = rewards_view
-        if config.max_episode_steps > 0:
-            timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
-            batch.reset_envs_device(timeout.to(torch.uint8))   # consoles not in the mask are untouched
-            done = done | timeout
+        if rewarder is None:
+            reward = rewards_view
+            if config.max_episode_steps > 0:
+                timeout = (episode_lengths >= float(config.max_episode_steps)) & ~done
+                batch.reset_envs_device(timeout.to(torch.uint8))   # consoles not in the mask are untouched
+                done = done | timeout
+        else:
+            reward = rewarder.compute(ram, pad, done)
+            if config.max_episode_steps > 0:
+                done = done | (episode_lengths >= float(config.max_episode_steps))
+            reset_mask = done.to(torch.uint8)
+            batch.reset_envs_device(reset_mask)
+            rewarder.reset_where(reset_mask, ram)              # from the post-reset RAM
         rewards_buf[t].copy_(reward)
         next_done.copy_(done.float())
         episode_returns.add_(reward)
@@ -550,6 +650,7 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
              "wall_s": 0.0, "log": [], "per_update": [], "graph_updates": 0}
     graph = None
     step_ms = None   # step + restore kernel time per rollout step, from the eager first rollout
+    progress = _progress_bar(config.progress_bar, global_step + num_updates * rollout_timesteps, global_step)
     t_start = time.perf_counter()
     for update in range(1, num_updates + 1):
         # The first rollout runs eagerly (HIP-event timing of the step kernel,
@@ -572,6 +673,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
                 if record is not None:
                     record(t, mask_table[actions_buf[t]], rewards_buf[t], next_done.bool())
         global_step += rollout_timesteps
+        if progress is not None:
+            progress.update(rollout_timesteps)   # per rollout: a graph replay runs all its steps at once
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         if not use_graph:
@@ -633,6 +736,8 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
             if config.save_checkpoints:
                 _save_checkpoint(config.checkpoint_path, model, optimizer, config, global_step)
     torch.cuda.synchronize()
+    if progress is not None:
+        progress.close()
     stats["wall_s"] = time.perf_counter() - t_start
     stats["global_step"] = global_step
     if config.save_checkpoints and num_updates > 0:
@@ -641,7 +746,20 @@ def train_native_ppo(config: NativePPOConfig, resume_from: str | None = None, *,
     return stats
 
 
-def parse_args() -> tuple[NativePPOConfig, str | None]:
+def _progress_bar(enabled: bool, total: int, initial: int):
+    """A tqdm bar over env-steps when asked for and tqdm is importable (the
+    reference's --progress-bar, native_ppo.py:606-613); else None."""
+    if not enabled:
+        return None
+    try:
+        from tqdm.auto import tqdm
+    except ImportError:
+        print("progress bar requested but tqdm is not importable; the update log lines remain")
+        return None
+    return tqdm(total=total, initial=min(initial, total), desc="native PPO", unit="env-steps")
+
+
+def parse_args(argv: Sequence[str] | None = None) -> tuple[NativePPOConfig, str | None]:
     p = argparse.ArgumentParser(description="Train with the GPU-resident PPO path on the MI355X console.")
     p.add_argument("rom_path")
     p.add_argument("--num-envs", type=int, default=1024)
@@ -663,13 +781,19 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
     p.add_argument("--vf-coef", type=float, default=0.5)
     p.add_argument("--max-grad-norm", type=float, default=0.5)
     p.add_argument("--hidden-size", type=int, default=256)
-    p.add_argument("--reward-mode", default="minimal", choices=["minimal"])
+    p.add_argument("--reward-mode", default="minimal", choices=["minimal", "smart"])
+    p.add_argument("--flag-bonus", type=float, default=None, help="override SmartMarioReward's flag bonus (smart mode)")
+    p.add_argument("--finish-zone-bonus", type=float, default=None,
+                   help="override SmartMarioReward's finish-zone bonus (smart mode)")
+    p.add_argument("--death-penalty", type=float, default=None,
+                   help="override SmartMarioReward's death penalty (smart mode)")
     p.add_argument("--init", default="orthogonal", choices=["orthogonal", "xavier"])
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--checkpoint-path", default="nesle_native_ppo.pt")
     p.add_argument("--resume-from", default=None)
     p.add_argument("--log-interval", type=int, default=1)
-    a = p.parse_args()
+    p.add_argument("--progress-bar", action="store_true")
+    a = p.parse_args(argv)
     if a.reset_state_path and a.reset_state_paths:
         raise SystemExit("Pass either --reset-state-path or --reset-state-paths, not both.")
     cfg = NativePPOConfig(
@@ -679,7 +803,9 @@ def parse_args() -> tuple[NativePPOConfig, str | None]:
         max_episode_steps=a.max_episode_steps, learning_rate=a.learning_rate, gamma=a.gamma,
         gae_lambda=a.gae_lambda, clip_coef=a.clip_coef, ent_coef=a.ent_coef, vf_coef=a.vf_coef,
         max_grad_norm=a.max_grad_norm, hidden_size=a.hidden_size, reward_mode=a.reward_mode,
-        init=a.init, seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval)
+        flag_bonus=a.flag_bonus, finish_zone_bonus=a.finish_zone_bonus, death_penalty=a.death_penalty,
+        init=a.init, seed=a.seed, checkpoint_path=a.checkpoint_path, log_interval=a.log_interval,
+        progress_bar=a.progress_bar)
     return cfg, a.resume_from
 
 

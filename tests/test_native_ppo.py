@@ -154,13 +154,6 @@ def test_ppo_head_refuses_host_tensors_before_any_launch():
     assert b"null" in L.nesle_last_error()
 
 
-def test_shaped_reward_mode_is_refused():
-    """Only the in-kernel reward rule trains here; the reference's shaped SMB
-    reward ("smart") is refused before any device work."""
-    with pytest.raises(ValueError, match="reward_mode"):
-        P.train_native_ppo(P.NativePPOConfig("none.nes", num_envs=64, n_steps=128, reward_mode="smart"))
-
-
 def test_explained_variance_closed_forms():
     g = torch.Generator().manual_seed(5)
     ret = torch.rand(1000, generator=g)
