@@ -468,7 +468,8 @@ def run_census(rom: bytes, snaps: list[bytes], levels: np.ndarray | None, done_i
     b.close()
     it = max(totals["iterations"], 1)
     per_it = {k: totals[k] / it for k in totals if k not in ("waves", "iterations", "census_kernel_us",
-                                                             "instructions")}
+                                                             "instructions", "distinct_entries", "distinct_samples")}
+    per_it["distinct_entries"] = totals["distinct_entries"] / max(totals["distinct_samples"], 1)
     waves = max(totals["waves"], 1)
     plain_ms = float(np.mean(ms_plain))
     return {

@@ -165,7 +165,7 @@ enum : std::uint32_t {
     kIoRead,             // wave-iterations with an I/O or PRG RAM read
     kIoReadSlow,         // ... through the branchy register read (not $2002/$4016)
     kActiveLanes,        // sum over wave-iterations of lanes still running frames
-    kDistinctEntries,    // sum over wave-iterations of distinct microcode entries among those lanes
+    kDistinctEntries,    // sum over sampled wave-iterations (every 16th) of distinct microcode entries among those lanes
     kCyclesLoop,         // shader clock, loop entry to exit, summed over waves
     kCyclesRare,         // ... inside the rare path (including the decode redone after it)
     kCyclesIoRead,       // ... inside the I/O read side path
@@ -174,6 +174,7 @@ enum : std::uint32_t {
     kLanesIoRead,        // lane events: I/O reads
     kLanesIoReadSlow,    // lane events: I/O reads through the branchy path
     kExits,              // rare wave-iterations after which the wave left the loop
+    kDistinctSamples,    // wave-iterations sampled for kDistinctEntries
     kCount = 32
 };
 }  // namespace census

@@ -282,10 +282,7 @@ struct Console {
         io = shifting ? ((io_n & 0xF000FFFFu) | ((sh >> 1) << 16) | ((n + 1) << 24)) : io_n;
         flags = r2002 ? (flags & ~(kNmiPending | kWToggle)) : flags;
         std::uint32_t v = r2002 ? v2002 : (0x40 | bit);
-        if (!r2002 && !r4016) {
-            v = io_rd(addr);
-            vmem_settled();
-        }
+        if (!r2002 && !r4016) v = io_rd(addr);   // the compiler waits for its load where v is used
         return v;
     }
 
@@ -857,7 +854,10 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         if constexpr (kStats == 3) {
             cz.v[census::kIterations] += 1;
             cz.lanes(census::kActiveLanes, active);
-            cz.v[census::kDistinctEntries] += WaveCensus::distinct(mi, active);
+            if ((cz.v[census::kIterations] & 15) == 0) {   // sampled: the count costs a loop of ballots
+                cz.v[census::kDistinctEntries] += WaveCensus::distinct(mi, active);
+                cz.v[census::kDistinctSamples] += 1;
+            }
             cz.count(census::kRare, rare);
             cz.count(census::kRareIoWrite, io_write);
             cz.count(census::kRareSide, side);
@@ -1035,10 +1035,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             slices(active ? op : mc::kNopEntry);
             address(op, b1, b2, c.regs);
         }
-        if constexpr (kStats == 3) {
-            vmem_settled();   // the redone decode's load is part of the rare cost
-            cz.v[census::kCyclesRare] += clock64() - t_rare;
-        }
+        if constexpr (kStats == 3) cz.v[census::kCyclesRare] += clock64() - t_rare;
     }
     if constexpr (kStats == 3) {
         cz.v[census::kCyclesLoop] += clock64() - t_loop;

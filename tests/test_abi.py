@@ -94,3 +94,16 @@ def test_null_handles_are_rejected():
     assert L.nesle_step(None, 0, 0) == abi.EINVAL
     assert L.nesle_reset(None) == abi.EINVAL
     assert L.nesle_num_envs(None) == 0 and L.nesle_device_id(None) == -1
+
+
+def test_census_field_names_follow_the_header_enum():
+    """abi.CENSUS_FIELDS names the census slots in the order of the census
+    enum in nesle_amd/csrc/nes_layout.h (k-prefixed CamelCase)."""
+    import re
+
+    text = (abi.LIB_PATH.parent / "csrc" / "nes_layout.h").read_text()
+    body = text.split("namespace census {", 1)[1].split("kCount", 1)[0]
+    body = re.sub(r"//[^\n]*", "", body)
+    names = re.findall(r"\bk([A-Z][A-Za-z0-9]*)\b", body)
+    snake = [re.sub(r"(?<!^)(?=[A-Z])", "_", n).lower() for n in names]
+    assert snake == list(abi.CENSUS_FIELDS)
