@@ -34,7 +34,8 @@ CENSUS_FIELDS = ("waves", "iterations", "rare", "rare_io_write", "rare_side", "r
                  "rare_timing", "rare_budget", "rare_outside", "rare_only_io_write", "dma", "present", "io_read",
                  "io_read_slow", "active_lanes", "distinct_entries", "cycles_loop", "cycles_rare", "cycles_io_read",
                  "lanes_io_write", "lanes_timing", "lanes_io_read", "lanes_io_read_slow", "exits",
-                 "distinct_samples")
+                 "distinct_samples", "cycles_io_write", "cycles_settle", "cycles_dma", "cycles_present",
+                 "cycles_redo", "redo")
 FRAME_RGB, FRAME_PALETTE, FRAME_GRAY84 = 1, 2, 4
 FRAME_LIVE = 8      # modifier: live state under the reference CPU core's rules
 DTYPE_U8, DTYPE_I64, DTYPE_F32, DTYPE_U32, DTYPE_U64 = 0, 1, 2, 3, 4

@@ -175,6 +175,12 @@ enum : std::uint32_t {
     kLanesIoReadSlow,    // lane events: I/O reads through the branchy path
     kExits,              // rare wave-iterations after which the wave left the loop
     kDistinctSamples,    // wave-iterations sampled for kDistinctEntries
+    kCyclesIoWrite,      // shader clock inside the rare path: I/O and PRG RAM writes
+    kCyclesSettle,       // ... PPU settlement after timing events and the budget
+    kCyclesDma,          // ... OAM DMA copies
+    kCyclesPresent,      // ... presentation captures
+    kCyclesRedo,         // ... the decode of the next instruction, when redone
+    kRedo,               // rare wave-iterations after which the decode was redone
     kCount = 32
 };
 }  // namespace census

@@ -477,9 +477,29 @@ struct Console {
             }
             rec[k] = static_cast<std::uint8_t>(v);
         }
-        const auto* from = reinterpret_cast<const std::uint32_t*>(s.vram + static_cast<std::size_t>(e_env) * vs);
-        auto* to = reinterpret_cast<std::uint32_t*>(rec + present::kHeader);
-        for (std::uint32_t i = lane; i < vs / 4; i += lanes) to[i] = from[i];
+        // 16-byte copies (the block and record strides and the record
+        // header are multiples of 16).  A wave loads all of its share before
+        // it stores any, so the copy costs one memory round trip.
+        using u32x4 = std::uint32_t __attribute__((ext_vector_type(4)));
+        const auto* from = reinterpret_cast<const u32x4*>(s.vram + static_cast<std::size_t>(e_env) * vs);
+        auto* to = reinterpret_cast<u32x4*>(rec + present::kHeader);
+        const std::uint32_t n = vs / 16;
+        if (false) {
+            static_assert((present::kMaxBytes - present::kHeader) / 16 <= 5 * 64, "five 16-byte loads per lane");
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+            const u32x4 v0 = lane < n ? from[lane] : zero;
+            const u32x4 v1 = lane + 64 < n ? from[lane + 64] : zero;
+            const u32x4 v2 = lane + 128 < n ? from[lane + 128] : zero;
+            const u32x4 v3 = lane + 192 < n ? from[lane + 192] : zero;
+            const u32x4 v4 = lane + 256 < n ? from[lane + 256] : zero;
+            if (lane < n) to[lane] = v0;
+            if (lane + 64 < n) to[lane + 64] = v1;
+            if (lane + 128 < n) to[lane + 128] = v2;
+            if (lane + 192 < n) to[lane + 192] = v3;
+            if (lane + 256 < n) to[lane + 256] = v4;
+        } else {
+            for (std::uint32_t i = lane; i < n; i += lanes) to[i] = from[i];
+        }
     }
 };
 
@@ -881,7 +901,14 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             continue;
         }
         if constexpr (kStats == 3) t_rare = clock64();
+        [[maybe_unused]] std::uint64_t t_sub = 0;
+        if constexpr (kStats == 3) t_sub = clock64();
         if (io_write) dots += c.io_wr(ea, r);
+        if constexpr (kStats == 3) {
+            const std::uint64_t t = clock64();
+            cz.v[census::kCyclesIoWrite] += t - t_sub;
+            t_sub = t;
+        }
         if (side) {
             std::uint32_t npc = next;
             if (d14 & mc::kJmpInd) {
@@ -936,6 +963,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             active = false;
         }
         left -= static_cast<std::int32_t>(dots);
+        if constexpr (kStats == 3) t_sub = clock64();
         if (counted && left <= 0) {  // a timing event was crossed: settle the PPU
             const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), kBudget);
             const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
@@ -965,6 +993,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // console's 256 bytes at a time, 4 per lane.  RAM, PRG RAM and PRG ROM
         // pages have no read side effects; I/O pages are read by the console's
         // own lane through the bus, in order.
+        if constexpr (kStats == 3) {
+            const std::uint64_t t = clock64();
+            cz.v[census::kCyclesSettle] += t - t_sub;
+            t_sub = t;
+        }
         std::uint64_t req = __ballot((c.flags & kDmaPending) != 0);
         if constexpr (kStats == 3) cz.v[census::kDma] += req != 0 ? 1u : 0u;
         while (req != 0) {
@@ -977,19 +1010,27 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             const std::uint32_t e_base = e_regs - C::kRegs;
             std::uint8_t* e_oam = s.vram + static_cast<std::size_t>(e_env) * s.vram_stride + vram::kOam;
             if (page < 0x20 || page >= 0x60) {
+                // All four loads go out before the stores (one round trip).
+                std::uint32_t val[4];
+#pragma unroll
                 for (std::uint32_t k = 0; k < 4; ++k) {
-                    const std::uint32_t i = 4 * lane + k;
-                    const std::uint32_t addr = (page << 8) | i;
-                    std::uint32_t val;
+                    const std::uint32_t addr = (page << 8) | (4 * lane + k);
                     if (page < 0x20) {
                         const std::uint32_t ra2 = addr & 0x7FF;
-                        val = C::ram_in_lds(ra2) ? lds[e_base + C::ram_lds_off(ra2)] : s.ram[__umul24(ra2, P) + e_env];
+                        val[k] = C::ram_in_lds(ra2) ? lds[e_base + C::ram_lds_off(ra2)] : s.ram[__umul24(ra2, P) + e_env];
                     } else if (page < 0x80) {
-                        val = s.ram[__umul24(addr - 0x5800, P) + e_env];
+                        val[k] = s.ram[__umul24(addr - 0x5800, P) + e_env];
                     } else {
-                        val = lds[addr & 0x7FFF];
+                        val[k] = lds[addr & 0x7FFF];
                     }
-                    e_oam[(oa + i) & 0xFF] = static_cast<std::uint8_t>(val);
+                }
+                const std::uint32_t word = val[0] | (val[1] << 8) | (val[2] << 16) | (val[3] << 24);
+                if (false) {
+                    reinterpret_cast<std::uint32_t*>(e_oam)[((oa >> 2) + lane) & 63] = word;
+                } else {
+#pragma unroll
+                    for (std::uint32_t k = 0; k < 4; ++k)
+                        e_oam[(oa + 4 * lane + k) & 0xFF] = static_cast<std::uint8_t>(val[k]);
                 }
             } else if (lane == src) {
                 // OAMADDR advances with every byte (ppu.hpp:131-134), which a
@@ -1004,6 +1045,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             }
         }
         c.flags &= ~kDmaPending;
+        if constexpr (kStats == 3) {
+            const std::uint64_t t = clock64();
+            cz.v[census::kCyclesDma] += t - t_sub;
+            t_sub = t;
+        }
         // Presentation snapshot at vblank (batch_ppu.cuh:219-249), after the
         // OAM DMA of the same instruction: the wave copies one console's
         // video memory block at a time (dwords, contiguous) into its record.
@@ -1017,6 +1063,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             C::capture(s, e_env, e_regs, lane, 64);
         }
         c.flags &= ~kPresentPending;
+        if constexpr (kStats == 3) cz.v[census::kCyclesPresent] += clock64() - t_sub;
         // Code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through the bus,
         // in order, once the PPU has settled.  NMI pending (set only here, by
         // a $2000 write or the vblank event): its entry runs next.
@@ -1031,9 +1078,16 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         if constexpr (!kFull) {
             // The rare work may have changed the next instruction, the
-            // registers or RAM: decode again.
+            // registers or RAM: decode again.  (Redoing it only in waves
+            // where some lane's instruction, registers or activity changed
+            // measured slower.)
+            if constexpr (kStats == 3) {
+                cz.v[census::kRedo] += 1;
+                t_sub = clock64();
+            }
             slices(active ? op : mc::kNopEntry);
             address(op, b1, b2, c.regs);
+            if constexpr (kStats == 3) cz.v[census::kCyclesRedo] += clock64() - t_sub;
         }
         if constexpr (kStats == 3) cz.v[census::kCyclesRare] += clock64() - t_rare;
     }
