@@ -869,8 +869,17 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const bool idle = (d14 & mc::kJmpAbs) && abs == pc0;
         const bool timing = counted && (left - static_cast<std::int32_t>(dots)) <= 0;
         const bool budget = kBudget && counted && in_frame >= max_instr;
-        const bool rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
-                          (next - 0x8000u) > 0x7FFDu;
+        // All RAM in LDS: the terms or-ed without short-circuit (no branch
+        // in the test; 1.6 % faster there); the split layout measured 4.5 %
+        // slower that way and keeps the short-circuit form.
+        bool rare;
+        if constexpr (kFull) {
+            rare = io_write | side | idle | ((d14 & mc::kIllegal) != 0) | timing | budget |
+                   ((next - 0x8000u) > 0x7FFDu);
+        } else {
+            rare = io_write || side || idle || (d14 & mc::kIllegal) || timing || budget ||
+                   (next - 0x8000u) > 0x7FFDu;
+        }
         if constexpr (kStats == 3) {
             cz.v[census::kIterations] += 1;
             cz.lanes(census::kActiveLanes, active);
