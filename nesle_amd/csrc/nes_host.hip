@@ -235,7 +235,7 @@ struct nesle_batch {
     // Step timing: three events per step (before the step kernel, between it
     // and the auto-reset's restore kernel, after that), folded into the
     // totals once the last has completed.
-    struct Marks { hipEvent_t start, stepped, reset; };
+    struct Marks { hipEvent_t start, stepped, reset; bool restored; };
     bool timing = false;
     std::vector<Marks> events;  // recorded, not yet folded
     std::vector<Marks> spare;
@@ -379,7 +379,9 @@ struct nesle_batch {
             hip_check(hipEventSynchronize(e.reset), "hipEventSynchronize");
             float step_ms = 0.0f, reset_ms = 0.0f;
             hip_check(hipEventElapsedTime(&step_ms, e.start, e.stepped), "hipEventElapsedTime");
-            hip_check(hipEventElapsedTime(&reset_ms, e.stepped, e.reset), "hipEventElapsedTime");
+            // A step without auto-reset launches no restore kernel: the gap
+            // between its two events is event overhead, not kernel time.
+            if (e.restored) hip_check(hipEventElapsedTime(&reset_ms, e.stepped, e.reset), "hipEventElapsedTime");
             timed_ms += step_ms;
             timed_reset_ms += reset_ms;
             ++timed_launches;
@@ -701,6 +703,7 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
         if (auto_reset != 0) hip_check(nesle::launch_reset(s, s.done, b->stream), "restore_kernel");
         if (b->timing) {
             hip_check(hipEventRecord(ev.reset, b->stream), "hipEventRecord");
+            ev.restored = auto_reset != 0;
             b->events.push_back(ev);
         }
         b->refresh_obs();
