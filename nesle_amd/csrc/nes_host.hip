@@ -656,7 +656,7 @@ int nesle_step(nesle_batch* b, int auto_reset, int stats_mode) {
     return guarded([&] {
         if (b == nullptr) throw InvalidArgument("null batch");
         if (stats_mode < 0 || stats_mode > 3) throw InvalidArgument("stats_mode must be 0, 1, 2 or 3");
-        if (b->synthetic) {   // no console runs: no instruction statistics (cuda_module.cu:669-671)
+        if (b->synthetic) {   // no console runs: no instruction statistics (cuda_module.cu:667-670)
             if (stats_mode != 0) throw std::runtime_error("step statistics need a console batch (one made from a ROM)");
             b->activate();
             hip_check(nesle::launch_synthetic_step(b->ds, b->cfg.frameskip, b->d_step_counts, true, b->stream),

@@ -83,7 +83,7 @@ def test_synthetic_batch_refuses_console_work():
 def test_two_argument_cuda_batch_is_the_synthetic_batch():
     """CudaBatch(num_envs, frameskip): name "cuda", step() moves x by the pad,
     step_device() only scores, step_stats is refused (cuda_module.cu:368-379,
-    546-565, 620-633, 669-671)."""
+    546-565, 620-633, 667-670)."""
     import torch
 
     from nesle_amd import load_cuda_core
