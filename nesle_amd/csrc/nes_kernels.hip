@@ -155,22 +155,58 @@ __global__ void __launch_bounds__(kBlock) save_blob_kernel(DeviceState s, std::u
     out[i] = v;
 }
 
-// RAM observation: [2048][pitch] interleaved -> [n][2048] env-major, through
-// a 64x64 LDS tile (coalesced on both sides).
+// RAM observation: [2048][pitch] interleaved -> [n][2048] env-major.  A
+// workgroup moves a tile of 256 consoles x 64 addresses in dwords: each lane
+// loads four consoles' bytes at four consecutive addresses (four coalesced
+// dword rows), transposes that 4x4 byte block in registers, and writes one
+// dword per console (four addresses) into the LDS tile; the tile is then
+// stored as dwords, 16 lanes per console row.  Loads stay inside the
+// console pitch (a multiple of 256); stores stop at the last console.
+constexpr std::uint32_t kObsEnvs = 256, kObsAddrs = 64;
+constexpr std::uint32_t kObsRow = kObsAddrs / 4 + 1;   // dwords per console row in LDS (odd: bank spread)
+
 __global__ void __launch_bounds__(kBlock) ram_obs_kernel(const std::uint8_t* __restrict__ ram,
                                                          std::uint8_t* __restrict__ obs, std::uint32_t n,
                                                          std::uint32_t pitch) {
-    __shared__ std::uint8_t tile[64][65];
-    const std::uint32_t env0 = blockIdx.x * 64, addr0 = blockIdx.y * 64;
-    const std::uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    for (std::uint32_t r = ty; r < 64; r += 4) {
-        const std::uint32_t env = env0 + tx;
-        tile[r][tx] = env < pitch ? ram[static_cast<std::size_t>(addr0 + r) * pitch + env] : 0;
+    __shared__ std::uint32_t tile[kObsEnvs * kObsRow];
+    const std::uint32_t env0 = blockIdx.x * kObsEnvs, addr0 = blockIdx.y * kObsAddrs;
+    const std::uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Wave w takes addresses addr0 + 16w .. +15, four at a time; lane l takes
+    // consoles env0 + 4l .. 4l + 3.
+    const std::uint8_t* src = ram + static_cast<std::size_t>(addr0 + 16 * wave) * pitch + env0 + 4 * lane;
+#pragma unroll
+    for (std::uint32_t g = 0; g < 4; ++g) {
+        const std::uint8_t* at = src + static_cast<std::size_t>(4 * g) * pitch;
+        const std::uint32_t w0 = *reinterpret_cast<const std::uint32_t*>(at);
+        const std::uint32_t w1 = *reinterpret_cast<const std::uint32_t*>(at + pitch);
+        const std::uint32_t w2 = *reinterpret_cast<const std::uint32_t*>(at + 2 * static_cast<std::size_t>(pitch));
+        const std::uint32_t w3 = *reinterpret_cast<const std::uint32_t*>(at + 3 * static_cast<std::size_t>(pitch));
+        // w_a holds byte j = console 4l + j at address a; c_j holds console
+        // 4l + j's bytes at the four addresses.
+        const std::uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);
+        const std::uint32_t t1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);
+        const std::uint32_t t2 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+        const std::uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+        const std::uint32_t c[4] = {__builtin_amdgcn_perm(t2, t0, 0x05040100u), __builtin_amdgcn_perm(t2, t0, 0x07060302u),
+                                    __builtin_amdgcn_perm(t3, t1, 0x05040100u), __builtin_amdgcn_perm(t3, t1, 0x07060302u)};
+        // Write order rotated by lane >> 3, so that the 32 lanes of a
+        // half-wave hit 32 different banks.
+        const std::uint32_t col = 4 * wave + g;
+#pragma unroll
+        for (std::uint32_t i = 0; i < 4; ++i) {
+            const std::uint32_t j = (i + (lane >> 3)) & 3;
+            const std::uint32_t v = j == 0 ? c[0] : j == 1 ? c[1] : j == 2 ? c[2] : c[3];
+            tile[(4 * lane + j) * kObsRow + col] = v;
+        }
     }
     __syncthreads();
-    for (std::uint32_t r = ty; r < 64; r += 4) {
-        const std::uint32_t env = env0 + r;
-        if (env < n) obs[static_cast<std::size_t>(env) * kRamBytes + addr0 + tx] = tile[tx][r];
+    const std::uint32_t c16 = threadIdx.x & 15;
+#pragma unroll 4
+    for (std::uint32_t e = threadIdx.x >> 4; e < kObsEnvs; e += kBlock / 16) {
+        const std::uint32_t env = env0 + e;
+        if (env < n)
+            *reinterpret_cast<std::uint32_t*>(obs + static_cast<std::size_t>(env) * kRamBytes + addr0 + 4 * c16) =
+                tile[e * kObsRow + c16];
     }
 }
 
@@ -345,7 +381,9 @@ hipError_t launch_save_blob(const DeviceState& s, std::uint32_t env, std::uint8_
 }
 
 hipError_t launch_ram_obs(const DeviceState& s, std::uint8_t* obs, hipStream_t stream) {
-    const dim3 grid((s.n + 63) / 64, kRamBytes / 64);
+    // The loads cover whole 256-console groups: the pitch is a multiple of 256.
+    if (s.pitch % kObsEnvs != 0 || s.pitch < s.n) return hipErrorInvalidValue;
+    const dim3 grid((s.n + kObsEnvs - 1) / kObsEnvs, kRamBytes / kObsAddrs);
     ram_obs_kernel<<<grid, dim3(kBlock), 0, stream>>>(s.ram, obs, s.n, s.pitch);
     return hipGetLastError();
 }
