@@ -989,15 +989,17 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
                 if (fl == 0) active = false;
             }
         }
-        if constexpr (!kBudget && !kFull) {
+        if constexpr (!kFull) {
             // Vblank rendezvous: a console that has just reached vblank waits
             // (runs the NOP entry, its time stopped) until every running
             // console of its wave has reached it too; then all take their NMI
             // together, so the handler's I/O writes, OAM DMA and captures
             // share rare-path entries instead of each console entering alone.
             // Waiting changes no console's results.  Every running console
-            // reaches its next vblank within a frame, and the wave resumes as
-            // soon as none is left running, so the wait always ends.  (With
+            // reaches its next vblank within a frame of PPU time (a frame the
+            // instruction budget ends early leaves the PPU running), or
+            // finishes its frames, and the wave resumes as soon as none is
+            // left running, so the wait always ends.  (With
             // all RAM in LDS a wave holds at most 32 consoles and waiting
             // costs more than it saves: 15.28 vs 15.06 ms at 4,096.)
             if (at_vblank && active) {
