@@ -574,3 +574,56 @@ def test_poke_ram_envs_writes_one_byte_per_console():
     with pytest.raises(ValueError):
         abi.lib()  # the library is loaded; a null values pointer is an argument error
         abi._check(abi.lib().nesle_poke_ram_envs(b.h, 0x12, None, 0))
+
+
+def test_split_batch_with_consoles_at_different_frame_phases():
+    """The split layout holds each console that reaches vblank until every
+    running console of its wave has (the NMI handlers then run together).
+    Consoles loaded from states saved in the middle of a frame reach vblank
+    at very different points of a step than consoles at a frame boundary:
+    16,384 consoles, a third of them (every third console, so each wave has
+    both kinds) loaded with one of four mid-frame states, the rest from
+    power-on, six steps at frame-skip 4 with the x-delta reward; every
+    step's rewards, dones and instruction counts, and the final states of
+    sampled consoles, equal oracle consoles given the same states."""
+    rom = synthrom.make_rom(2026).rom
+    reward = dict(kind=1, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI, done_addr=synthrom.DONE_BYTE, clip=15,
+                  time_penalty=0.01)
+    states = []
+    for k, (frames, extra) in enumerate([(12, 1500), (20, 3700), (31, 5200), (45, 6900)]):
+        o = O.Oracle(rom)
+        for f in range(frames):
+            o.step(int(masks_for(40 + k, 1, f)[0]), 1)
+        for _ in range(extra):                     # into the middle of the next frame
+            o.step_instruction()
+        states.append(o.save())
+    for st in states:
+        dot = int(np.frombuffer(st[O.OFF["frame_dot"]:O.OFF["frame_dot"] + 4].tobytes(), np.uint32)[0])
+        assert 1000 < dot < 88000, dot                 # not at a frame boundary
+    n, steps = 16384, 6
+    rng = np.random.default_rng(41)
+    which = np.full(n, -1)
+    which[::3] = rng.integers(0, len(states), which[::3].size)
+    sample = sorted({0, 1, 2, 3, 63, 64, 8190, 8191, n - 1, *rng.integers(0, n, 9).tolist()})
+    say(f"[gpu] split batch, mixed frame phases: N={n} steps={steps} sample={sample}")
+    b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                  done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.01)
+    for k, st in enumerate(states):
+        b.load_state(st, (which == k).astype(np.uint8))
+    ob = OracleBatch(rom, sample, reward=reward)
+    for e, c in zip(sample, ob.cons):
+        if which[e] >= 0:
+            c.load(states[which[e]])
+    for k in range(steps):
+        m = masks_for(42, n, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins, rew, don = ob.step(m, 4)
+        got_ins = b.host(abi.VIEW_INSTRUCTIONS)[sample].astype(np.int64)
+        got_rew, got_don = b.host(abi.VIEW_REWARDS)[sample], b.host(abi.VIEW_DONES)[sample]
+        assert np.array_equal(got_ins, ins), (k, got_ins, ins)
+        assert np.array_equal(got_rew, rew) and np.array_equal(got_don, don), (k, got_rew, rew, got_don, don)
+    for e, st in zip(sample, ob.states()):
+        got = b.save_state(e)
+        assert np.array_equal(got, st), f"console {e}: {first_diff(got, st)}"
+    b.close()
