@@ -11,14 +11,17 @@
 
 namespace nesle {
 
-// Console RAM straight from HBM (kernels other than the step kernel).
-struct GlobalRam {
-    const DeviceState& s;
+// Console RAM straight from HBM.  `State` is DeviceState, or the step
+// kernel's view of it in the kernel-argument segment.
+template <typename State>
+struct GlobalRamOf {
+    const State& s;
     std::uint32_t env;
     __device__ __forceinline__ std::uint32_t operator()(std::uint32_t a) const {
         return s.ram[static_cast<std::size_t>(a & 0x7FF) * s.pitch + env];
     }
 };
+using GlobalRam = GlobalRamOf<DeviceState>;
 
 // ---- reward / done (batch_step.cuh:41-106; x-delta rule documented in
 //      nes_layout.h).  `ram` is any callable returning console RAM bytes.
@@ -41,8 +44,8 @@ __device__ __forceinline__ void reward_seed(const DeviceState& s, std::uint32_t 
     }
 }
 
-template <typename Ram>
-__device__ __forceinline__ void reward_apply(const DeviceState& s, std::uint32_t e, const Ram& ram, float* reward,
+template <typename State, typename Ram>
+__device__ __forceinline__ void reward_apply(const State& s, std::uint32_t e, const Ram& ram, float* reward,
                                              std::uint32_t* done) {
     if (s.reward_kind == kRewardSmb) {
         std::int32_t x, t;

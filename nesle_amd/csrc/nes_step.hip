@@ -126,6 +126,20 @@ __device__ __forceinline__ std::uint32_t xcd_block(std::uint32_t b, std::uint32_
 // also wait for the store the previous iteration just issued.
 __device__ __forceinline__ void vmem_settled() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// The kernel's DeviceState where the launch placed it, in the kernel-argument
+// segment (constant address space): a field read through it is a scalar load.
+using KState = const __attribute__((address_space(4))) DeviceState;
+
+// The same pointer, opaque to the optimiser.  Fields read through the result
+// are loaded where they are used instead of being held in scalar registers
+// across the loop: the rare work and the write-back read about forty of them,
+// and held for the whole loop they took the registers of the hot path's
+// constants, which were then materialised again on every iteration.
+__device__ __forceinline__ KState* reload(KState* p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
 // Bitwise select: bits of `a` where `m` is set, else bits of `b` (v_bfi_b32).
 __device__ __forceinline__ std::uint32_t sel(std::uint32_t m, std::uint32_t a, std::uint32_t b) {
     return (a & m) | (b & ~m);
@@ -160,7 +174,9 @@ struct Console {
     // Offset of stack byte $0100 + SP - 2 is SP + kStk (SP >= 0x82 in split mode).
     static constexpr std::uint32_t kStk = kFull ? 0xFEu : static_cast<std::uint32_t>(-0x82);
 
-    const DeviceState& s;
+    // The launch's state: reloaded (`reload`) at the start of the rare work, so
+    // the side paths and the rare work read its fields where they use them.
+    KState* s;
     std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
     // Hot state in VGPRs: CPU registers, `flags` (NMI latch, pending OAM DMA,
@@ -217,25 +233,25 @@ struct Console {
     __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return __umul24(row, pitch) + env; }
     // This console's video memory block (env-major).
     __device__ __forceinline__ std::uint8_t* vmem() const {
-        return s.vram + static_cast<std::size_t>(env) * s.vram_stride;
+        return s->vram + static_cast<std::size_t>(env) * s->vram_stride;
     }
     __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t ra) const {
         if (ram_in_lds(ra)) return lds[base + ram_lds_off(ra)];
-        return s.ram[goff(ra)];
+        return s->ram[goff(ra)];
     }
     __device__ __forceinline__ void ram_wr(std::uint32_t ra, std::uint32_t val) const {
         if (ram_in_lds(ra)) {
             lds[base + ram_lds_off(ra)] = static_cast<std::uint8_t>(val);
         } else {
-            s.ram[goff(ra)] = static_cast<std::uint8_t>(val);
+            s->ram[goff(ra)] = static_cast<std::uint8_t>(val);
         }
     }
 
     // ---- PPU memory (ppu.hpp:280-338) -------------------------------------------
     __device__ std::uint32_t nt_index(std::uint32_t addr) const {
         const std::uint32_t i = (addr - 0x2000) & 0x0FFF;
-        if (s.nt_mode == 2) return i;
-        if (s.nt_mode == 0) return i & 0x07FF;
+        if (s->nt_mode == 2) return i;
+        if (s->nt_mode == 0) return i & 0x07FF;
         return (i & 0x03FF) | ((i & 0x0800) >> 1);
     }
     __device__ static std::uint32_t pal_index(std::uint32_t addr) {
@@ -245,8 +261,8 @@ struct Console {
     __device__ std::uint32_t vram_rd(std::uint32_t addr) const {
         addr &= 0x3FFF;
         if (addr < 0x2000) {
-            if (s.chr_size != 0) return s.chr_rom[addr % s.chr_size];
-            return s.chr_ram[goff(addr & 0x1FFF)];
+            if (s->chr_size != 0) return s->chr_rom[addr % s->chr_size];
+            return s->chr_ram[goff(addr & 0x1FFF)];
         }
         if (addr < 0x3F00) {
             if (addr >= 0x3000) addr -= 0x1000;
@@ -257,7 +273,7 @@ struct Console {
     __device__ void vram_wr(std::uint32_t addr, std::uint32_t val) const {
         addr &= 0x3FFF;
         if (addr < 0x2000) {
-            if (s.chr_size == 0) s.chr_ram[goff(addr & 0x1FFF)] = static_cast<std::uint8_t>(val);
+            if (s->chr_size == 0) s->chr_ram[goff(addr & 0x1FFF)] = static_cast<std::uint8_t>(val);
             return;
         }
         if (addr < 0x3F00) {
@@ -289,7 +305,7 @@ struct Console {
     // ---- I/O space $2000-$5FFF (console.hpp:49-101, ppu.hpp:84-134,340-396,
     //      controller.hpp:20-47) ----------------------------------------------------
     __device__ std::uint32_t io_rd(std::uint32_t addr) {
-        if (addr >= 0x6000) return s.ram[goff(addr - 0x5800)];   // PRG RAM
+        if (addr >= 0x6000) return s->ram[goff(addr - 0x5800)];   // PRG RAM
         if (addr < 0x4000) {
             const std::uint32_t reg = addr & 7;
             if (reg == 2) {
@@ -336,7 +352,7 @@ struct Console {
             }
             return 0x41;
         }
-        if (addr < 0x4018) return s.apu_io[goff(addr - 0x4000)];
+        if (addr < 0x4018) return s->apu_io[goff(addr - 0x4000)];
         return 0;
     }
 
@@ -386,7 +402,7 @@ struct Console {
     // Returns the extra PPU dots the write costs (OAM DMA: 513 CPU cycles).
     __device__ std::uint32_t io_wr(std::uint32_t addr, std::uint32_t val) {
         if (addr >= 0x6000) {   // PRG RAM
-            s.ram[goff(addr - 0x5800)] = static_cast<std::uint8_t>(val);
+            s->ram[goff(addr - 0x5800)] = static_cast<std::uint8_t>(val);
             return 0;
         }
         if (addr < 0x4000) {
@@ -394,7 +410,7 @@ struct Console {
             return 0;
         }
         if (addr >= 0x4018) return 0;
-        s.apu_io[goff(addr - 0x4000)] = static_cast<std::uint8_t>(val);
+        s->apu_io[goff(addr - 0x4000)] = static_cast<std::uint8_t>(val);
         if (addr == 0x4014) {  // copied by the wave right after this instruction
             w8(reg::kDmaPage, val);
             flags |= kDmaPending;
@@ -415,7 +431,7 @@ struct Console {
     __device__ std::uint32_t bus_rd(std::uint32_t addr) {
         if (addr < 0x2000) return ram_rd(addr & 0x7FF);
         if (addr >= 0x8000) return lds[addr & 0x7FFF];
-        if (addr >= 0x6000) return s.ram[goff(addr - 0x5800)];
+        if (addr >= 0x6000) return s->ram[goff(addr - 0x5800)];
         return io_rd(addr) & 0xFF;
     }
 
@@ -439,16 +455,16 @@ struct Console {
                 if (vblank != nullptr) *vblank = true;
                 if (!(status & 0x80) && (ctrl & 0x80)) flags |= kNmiPending;
                 status |= 0x80;
-                if (s.present != nullptr && (every_vblank || r32(reg::kFramesLeft) <= fo + 1))
+                if (s->present != nullptr && (every_vblank || r32(reg::kFramesLeft) <= fo + 1))
                     flags |= kPresentPending;   // captured after the instruction
             }
             if (crossed(kPreRenderDot)) {
                 status &= 0x1F;
                 flags &= ~kNmiPending;
-                if (s.present != nullptr) {   // frame-start scroll/ctrl of the next snapshot
-                    s.lat_sx[env] = static_cast<std::uint8_t>(r8(reg::kScrollX));
-                    s.lat_sy[env] = static_cast<std::uint8_t>(r8(reg::kScrollY));
-                    s.lat_ctrl[env] = static_cast<std::uint8_t>(ctrl);
+                if (s->present != nullptr) {   // frame-start scroll/ctrl of the next snapshot
+                    s->lat_sx[env] = static_cast<std::uint8_t>(r8(reg::kScrollX));
+                    s->lat_sy[env] = static_cast<std::uint8_t>(r8(reg::kScrollY));
+                    s->lat_ctrl[env] = static_cast<std::uint8_t>(ctrl);
                 }
             }
         }
@@ -461,16 +477,16 @@ struct Console {
     // ctrl latched at the last pre-render line, the current ones, the mask,
     // then the video memory block.  `lane`/`lanes`: the copy is shared by
     // `lanes` cooperating lanes (1 when the console's own lane does it alone).
-    __device__ static void capture(const DeviceState& s, std::uint32_t e_env, std::uint32_t e_regs,
+    __device__ static void capture(KState* s, std::uint32_t e_env, std::uint32_t e_regs,
                                    std::uint32_t lane, std::uint32_t lanes) {
-        const std::uint32_t vs = s.vram_stride;
-        std::uint8_t* rec = s.present + static_cast<std::size_t>(e_env) * (present::kHeader + vs);
+        const std::uint32_t vs = s->vram_stride;
+        std::uint8_t* rec = s->present + static_cast<std::size_t>(e_env) * (present::kHeader + vs);
         for (std::uint32_t k = lane; k < 7; k += lanes) {
             std::uint32_t v;
             switch (k) {
-                case 0: v = s.lat_sx[e_env]; break;
-                case 1: v = s.lat_sy[e_env]; break;
-                case 2: v = s.lat_ctrl[e_env]; break;
+                case 0: v = s->lat_sx[e_env]; break;
+                case 1: v = s->lat_sy[e_env]; break;
+                case 2: v = s->lat_ctrl[e_env]; break;
                 case 3: v = lds[e_regs + reg::kScrollX]; break;
                 case 4: v = lds[e_regs + reg::kScrollY]; break;
                 case 5: v = lds[e_regs + reg::kCtrl]; break;
@@ -482,7 +498,7 @@ struct Console {
         // header are multiples of 16).  A wave loads all of its share before
         // it stores any, so the copy costs one memory round trip.
         using u32x4 = std::uint32_t __attribute__((ext_vector_type(4)));
-        const auto* from = reinterpret_cast<const u32x4*>(s.vram + static_cast<std::size_t>(e_env) * vs);
+        const auto* from = reinterpret_cast<const u32x4*>(s->vram + static_cast<std::size_t>(e_env) * vs);
         auto* to = reinterpret_cast<u32x4*>(rec + present::kHeader);
         const std::uint32_t n = vs / 16;
         if (false) {
@@ -572,7 +588,8 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     }
     const std::uint32_t base = kLdsRam + (mine ? slot : (T >> 6) * L) * C::kStride;
     const std::uint32_t P = s.pitch;
-    C c{s, mine ? env : 0u, base, P};
+    // `s` is the kernel's first argument: it starts the kernel-argument segment.
+    C c{(KState*)__builtin_amdgcn_kernarg_segment_ptr(), mine ? env : 0u, base, P};
     std::uint32_t fd0 = 0, horizon0 = 0;
     if (mine) {
         // This console's RAM rows that live in LDS.
@@ -911,6 +928,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             left -= static_cast<std::int32_t>(dots);
             continue;
         }
+        c.s = reload(c.s);
         if constexpr (kStats == 3) t_rare = clock64();
         [[maybe_unused]] std::uint64_t t_sub = 0;
         if constexpr (kStats == 3) t_sub = clock64();
@@ -964,8 +982,8 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             in_frame += static_cast<std::uint32_t>(k);
             instructions += static_cast<std::uint32_t>(k);
             if constexpr (kStats == 2) {
-                atomicAdd(&s.prof_opcodes[0x4C], static_cast<unsigned long long>(k));
-                atomicAdd(&s.prof_pcs[pc0], static_cast<unsigned long long>(k));
+                atomicAdd(&c.s->prof_opcodes[0x4C], static_cast<unsigned long long>(k));
+                atomicAdd(&c.s->prof_pcs[pc0], static_cast<unsigned long long>(k));
             }
         }
         // An illegal opcode freezes the console (the NOP-like entry changed nothing).
@@ -1042,7 +1060,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             const std::uint32_t page = lds[e_regs + reg::kDmaPage];
             const std::uint32_t oa = lds[e_regs + reg::kOamAddr];
             const std::uint32_t e_base = e_regs - C::kRegs;
-            std::uint8_t* e_oam = s.vram + static_cast<std::size_t>(e_env) * s.vram_stride + vram::kOam;
+            std::uint8_t* e_oam = c.s->vram + static_cast<std::size_t>(e_env) * c.s->vram_stride + vram::kOam;
             if (page < 0x20 || page >= 0x60) {
                 // All four loads go out before the stores (one round trip).
                 std::uint32_t val[4];
@@ -1051,9 +1069,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
                     const std::uint32_t addr = (page << 8) | (4 * lane + k);
                     if (page < 0x20) {
                         const std::uint32_t ra2 = addr & 0x7FF;
-                        val[k] = C::ram_in_lds(ra2) ? lds[e_base + C::ram_lds_off(ra2)] : s.ram[__umul24(ra2, P) + e_env];
+                        val[k] = C::ram_in_lds(ra2) ? lds[e_base + C::ram_lds_off(ra2)] : c.s->ram[__umul24(ra2, P) + e_env];
                     } else if (page < 0x80) {
-                        val[k] = s.ram[__umul24(addr - 0x5800, P) + e_env];
+                        val[k] = c.s->ram[__umul24(addr - 0x5800, P) + e_env];
                     } else {
                         val[k] = lds[addr & 0x7FFF];
                     }
@@ -1094,7 +1112,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             preq &= preq - 1;
             const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
             const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
-            C::capture(s, e_env, e_regs, lane, 64);
+            C::capture(c.s, e_env, e_regs, lane, 64);
         }
         c.flags &= ~kPresentPending;
         if constexpr (kStats == 3) cz.v[census::kCyclesPresent] += clock64() - t_sub;
@@ -1125,9 +1143,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         if constexpr (kStats == 3) cz.v[census::kCyclesRare] += clock64() - t_rare;
     }
+    // The write-back reads the state's fields after the loop.
+    c.s = reload(c.s);
+    KState& es = *c.s;
     if constexpr (kStats == 3) {
         cz.v[census::kCyclesLoop] += clock64() - t_loop;
-        cz.flush(s.census, lane);
+        cz.flush(es.census, lane);
     }
 
     if (!mine) return;
@@ -1136,12 +1157,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     if (left != static_cast<std::int32_t>(c.r32(reg::kHorizon))) {
         c.w32(reg::kFrames,
               c.r32(reg::kFrames) + c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), true));
-        if (c.flags & kPresentPending) C::capture(s, env, base + C::kRegs, 0, 1);
+        if (c.flags & kPresentPending) C::capture(c.s, env, base + C::kRegs, 0, 1);
     }
 
     // Write the LDS-resident RAM rows and registers back to HBM.
     {
-        std::uint8_t* g = s.ram + env;
+        std::uint8_t* g = es.ram + env;
         auto unstage = [&](std::uint32_t ra, std::uint32_t at) {
             const std::uint32_t v4 = reinterpret_cast<const std::uint32_t*>(lds + base + at)[0];
             const std::size_t r = ra;
@@ -1159,47 +1180,47 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     }
     const std::uint32_t fd = c.r32(reg::kFrameDot);
     const std::uint32_t frames = c.r32(reg::kFrames);
-    s.pc[env] = static_cast<std::uint16_t>(c.pc);
-    s.a[env] = static_cast<std::uint8_t>(c.regs);
-    s.x[env] = static_cast<std::uint8_t>(c.regs >> 8);
-    s.y[env] = static_cast<std::uint8_t>(c.regs >> 16);
-    s.sp[env] = static_cast<std::uint8_t>(c.regs >> 24);
-    s.p[env] = static_cast<std::uint8_t>(c.p);
+    es.pc[env] = static_cast<std::uint16_t>(c.pc);
+    es.a[env] = static_cast<std::uint8_t>(c.regs);
+    es.x[env] = static_cast<std::uint8_t>(c.regs >> 8);
+    es.y[env] = static_cast<std::uint8_t>(c.regs >> 16);
+    es.sp[env] = static_cast<std::uint8_t>(c.regs >> 24);
+    es.p[env] = static_cast<std::uint8_t>(c.p);
     // Every CPU cycle is 3 PPU dots.
     const std::uint64_t advanced = static_cast<std::uint64_t>(frames) * kFrameDots + fd - fd0;
-    s.cycles[env] += advanced / 3;
-    s.frame[env] += frames;
-    s.frame_dot[env] = fd;
-    s.nmi_pending[env] = static_cast<std::uint8_t>((c.flags & kNmiPending) ? 1 : 0);
-    s.status[env] = static_cast<std::uint8_t>(c.status());
-    s.ctrl[env] = static_cast<std::uint8_t>(c.r8(reg::kCtrl));
-    s.mask[env] = static_cast<std::uint8_t>(c.r8(reg::kMask));
-    s.oam_addr[env] = static_cast<std::uint8_t>(c.r8(reg::kOamAddr));
-    s.open_bus[env] = static_cast<std::uint8_t>(c.open_bus());
-    s.read_buffer[env] = static_cast<std::uint8_t>(c.r8(reg::kReadBuffer));
-    s.v[env] = static_cast<std::uint16_t>(c.r16(reg::kV));
-    s.t[env] = static_cast<std::uint16_t>(c.r16(reg::kT));
-    s.fine_x[env] = static_cast<std::uint8_t>(c.r8(reg::kFineX));
-    s.w[env] = static_cast<std::uint8_t>((c.flags & kWToggle) ? 1 : 0);
-    s.scroll_x[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollX));
-    s.scroll_y[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollY));
-    s.c1_buttons[env] = static_cast<std::uint8_t>(c.buttons());
-    s.c1_shift[env] = static_cast<std::uint8_t>(c.c1_shift());
-    s.c1_count[env] = static_cast<std::uint8_t>(c.c1_count());
-    s.strobe[env] = static_cast<std::uint8_t>((c.flags & kStrobeBit) ? 1 : 0);
-    s.c2_count[env] = static_cast<std::uint8_t>(c.c2_count());
+    es.cycles[env] += advanced / 3;
+    es.frame[env] += frames;
+    es.frame_dot[env] = fd;
+    es.nmi_pending[env] = static_cast<std::uint8_t>((c.flags & kNmiPending) ? 1 : 0);
+    es.status[env] = static_cast<std::uint8_t>(c.status());
+    es.ctrl[env] = static_cast<std::uint8_t>(c.r8(reg::kCtrl));
+    es.mask[env] = static_cast<std::uint8_t>(c.r8(reg::kMask));
+    es.oam_addr[env] = static_cast<std::uint8_t>(c.r8(reg::kOamAddr));
+    es.open_bus[env] = static_cast<std::uint8_t>(c.open_bus());
+    es.read_buffer[env] = static_cast<std::uint8_t>(c.r8(reg::kReadBuffer));
+    es.v[env] = static_cast<std::uint16_t>(c.r16(reg::kV));
+    es.t[env] = static_cast<std::uint16_t>(c.r16(reg::kT));
+    es.fine_x[env] = static_cast<std::uint8_t>(c.r8(reg::kFineX));
+    es.w[env] = static_cast<std::uint8_t>((c.flags & kWToggle) ? 1 : 0);
+    es.scroll_x[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollX));
+    es.scroll_y[env] = static_cast<std::uint8_t>(c.r8(reg::kScrollY));
+    es.c1_buttons[env] = static_cast<std::uint8_t>(c.buttons());
+    es.c1_shift[env] = static_cast<std::uint8_t>(c.c1_shift());
+    es.c1_count[env] = static_cast<std::uint8_t>(c.c1_count());
+    es.strobe[env] = static_cast<std::uint8_t>((c.flags & kStrobeBit) ? 1 : 0);
+    es.c2_count[env] = static_cast<std::uint8_t>(c.c2_count());
     const bool fault = (c.flags & kFault) != 0;
-    s.fault[env] = static_cast<std::uint8_t>(fault ? 1 : 0);
+    es.fault[env] = static_cast<std::uint8_t>(fault ? 1 : 0);
 
     float reward = 0.0f;
     std::uint32_t done = 1;
-    if (!fault) reward_apply(s, env, GlobalRam{s, env}, &reward, &done);
-    s.rewards[env] = reward;
-    s.done[env] = static_cast<std::uint8_t>(done);
+    if (!fault) reward_apply(es, env, GlobalRamOf<KState>{es, env}, &reward, &done);
+    es.rewards[env] = reward;
+    es.done[env] = static_cast<std::uint8_t>(done);
     if constexpr (kStats != 0) {
-        s.stat_instructions[env] = instructions;
-        s.stat_frames[env] = frames;
-        s.stat_budget_hits[env] = c.r32(reg::kBudgetHits);
+        es.stat_instructions[env] = instructions;
+        es.stat_frames[env] = frames;
+        es.stat_budget_hits[env] = c.r32(reg::kBudgetHits);
     }
 }
 
