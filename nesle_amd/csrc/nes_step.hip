@@ -495,13 +495,16 @@ struct Console {
             rec[k] = static_cast<std::uint8_t>(v);
         }
         // 16-byte copies (the block and record strides and the record
-        // header are multiples of 16).  A wave loads all of its share before
-        // it stores any, so the copy costs one memory round trip.
+        // header are multiples of 16).  With all RAM in LDS a whole wave
+        // loads its share (at most five pieces per lane) before it stores
+        // any, one memory round trip per console; the split layout, whose
+        // waves capture together at the vblank rendezvous (capture_own),
+        // keeps the plain loop for the few consoles that capture alone.
         using u32x4 = std::uint32_t __attribute__((ext_vector_type(4)));
         const auto* from = reinterpret_cast<const u32x4*>(s->vram + static_cast<std::size_t>(e_env) * vs);
         auto* to = reinterpret_cast<u32x4*>(rec + present::kHeader);
         const std::uint32_t n = vs / 16;
-        if (false) {
+        if (kFull && lanes == 64) {
             static_assert((present::kMaxBytes - present::kHeader) / 16 <= 5 * 64, "five 16-byte loads per lane");
             const u32x4 zero = {0u, 0u, 0u, 0u};
             const u32x4 v0 = lane < n ? from[lane] : zero;
@@ -516,6 +519,34 @@ struct Console {
             if (lane + 256 < n) to[lane + 256] = v4;
         } else {
             for (std::uint32_t i = lane; i < n; i += lanes) to[i] = from[i];
+        }
+    }
+
+    // The same record, copied by the console's own lane with eight 16-byte
+    // loads in flight at a time: for the split layout's waves, whose
+    // consoles reach vblank together and capture in the same iteration.
+    __device__ static void capture_own(KState* s, std::uint32_t e_env, std::uint32_t e_regs) {
+        const std::uint32_t vs = s->vram_stride;
+        std::uint8_t* rec = s->present + static_cast<std::size_t>(e_env) * (present::kHeader + vs);
+        rec[0] = s->lat_sx[e_env];
+        rec[1] = s->lat_sy[e_env];
+        rec[2] = s->lat_ctrl[e_env];
+        rec[3] = lds[e_regs + reg::kScrollX];
+        rec[4] = lds[e_regs + reg::kScrollY];
+        rec[5] = lds[e_regs + reg::kCtrl];
+        rec[6] = lds[e_regs + reg::kMask];
+        using u32x4 = std::uint32_t __attribute__((ext_vector_type(4)));
+        const auto* from = reinterpret_cast<const u32x4*>(s->vram + static_cast<std::size_t>(e_env) * vs);
+        auto* to = reinterpret_cast<u32x4*>(rec + present::kHeader);
+        const std::uint32_t n = vs / 16;
+        constexpr std::uint32_t kPer = 8;
+        for (std::uint32_t i = 0; i < n; i += kPer) {
+            u32x4 v[kPer];
+#pragma unroll
+            for (std::uint32_t k = 0; k < kPer; ++k) v[k] = from[i + k < n ? i + k : n - 1];
+#pragma unroll
+            for (std::uint32_t k = 0; k < kPer; ++k)
+                if (i + k < n) to[i + k] = v[k];
         }
     }
 };
@@ -1104,17 +1135,39 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         // Presentation snapshot at vblank (batch_ppu.cuh:219-249), after the
         // OAM DMA of the same instruction: the wave copies one console's
-        // video memory block at a time (dwords, contiguous) into its record.
-        std::uint64_t preq = __ballot((c.flags & kPresentPending) != 0);
-        if constexpr (kStats == 3) cz.v[census::kPresent] += preq != 0 ? 1u : 0u;
-        while (preq != 0) {
-            const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(preq)) - 1);
-            preq &= preq - 1;
-            const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
-            const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
-            C::capture(c.s, e_env, e_regs, lane, 64);
+        // video memory block at a time (contiguous 16-byte pieces) into its
+        // record.  Split layout: a console waiting at the vblank rendezvous
+        // captures when the wave resumes (it runs nothing while it waits, so
+        // its video memory is what it was at vblank), and when eight or more
+        // capture together each lane copies its own console's record.
+        if constexpr (kFull) {
+            std::uint64_t preq = __ballot((c.flags & kPresentPending) != 0);
+            if constexpr (kStats == 3) cz.v[census::kPresent] += preq != 0 ? 1u : 0u;
+            while (preq != 0) {
+                const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(preq)) - 1);
+                preq &= preq - 1;
+                const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
+                const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
+                C::capture(c.s, e_env, e_regs, lane, 64);
+            }
+            c.flags &= ~kPresentPending;
+        } else {
+            const bool want = (c.flags & kPresentPending) != 0 && !parked;
+            std::uint64_t preq = __ballot(want);
+            if constexpr (kStats == 3) cz.v[census::kPresent] += preq != 0 ? 1u : 0u;
+            if (__popcll(preq) >= 8) {
+                if (want) C::capture_own(c.s, env, base + C::kRegs);
+            } else {
+                while (preq != 0) {
+                    const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(preq)) - 1);
+                    preq &= preq - 1;
+                    const std::uint32_t e_env = __builtin_amdgcn_readlane(c.env, src);
+                    const std::uint32_t e_regs = __builtin_amdgcn_readlane(c.base, src) + C::kRegs;
+                    C::capture(c.s, e_env, e_regs, lane, 64);
+                }
+            }
+            if (want) c.flags &= ~kPresentPending;
         }
-        c.flags &= ~kPresentPending;
         if constexpr (kStats == 3) cz.v[census::kCyclesPresent] += clock64() - t_sub;
         // Code outside PRG ROM (RAM, PRG RAM, I/O) is fetched through the bus,
         // in order, once the PPU has settled.  NMI pending (set only here, by
