@@ -179,6 +179,11 @@ struct Console {
     KState* s;
     std::uint32_t env, base, pitch;
     std::uint32_t nmi_vec, brk_vec;
+    // Split layout: this console's video memory block, held for the loop
+    // (the I/O side path's `$2004` and `$2007` reads then need no scalar
+    // loads; with all RAM in LDS it is computed where it is used, which
+    // measured faster there).
+    std::uint8_t* vm = nullptr;
     // Hot state in VGPRs: CPU registers, `flags` (NMI latch, pending OAM DMA,
     // fault, write toggle, strobe, pad 1 buttons) and `io` (open bus, status,
     // pad shift state).  The other PPU registers live in the console's LDS
@@ -233,7 +238,8 @@ struct Console {
     __device__ __forceinline__ std::uint32_t goff(std::uint32_t row) const { return __umul24(row, pitch) + env; }
     // This console's video memory block (env-major).
     __device__ __forceinline__ std::uint8_t* vmem() const {
-        return s->vram + static_cast<std::size_t>(env) * s->vram_stride;
+        if constexpr (kFull) return s->vram + static_cast<std::size_t>(env) * s->vram_stride;
+        return vm;
     }
     __device__ __forceinline__ std::uint32_t ram_rd(std::uint32_t ra) const {
         if (ram_in_lds(ra)) return lds[base + ram_lds_off(ra)];
@@ -621,6 +627,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     const std::uint32_t P = s.pitch;
     // `s` is the kernel's first argument: it starts the kernel-argument segment.
     C c{(KState*)__builtin_amdgcn_kernarg_segment_ptr(), mine ? env : 0u, base, P};
+    if constexpr (!kFull) c.vm = s.vram + static_cast<std::size_t>(c.env) * s.vram_stride;
     std::uint32_t fd0 = 0, horizon0 = 0;
     if (mine) {
         // This console's RAM rows that live in LDS.
