@@ -94,8 +94,9 @@ constexpr std::uint32_t kDmaPending = 1, kNmiPending = 2, kFault = 4, kPresentPe
 static_assert(kNmiPending == mc::kClearNmi, "NMI flag and clear bit must match");
 // The PPU and pad registers every I/O read touches live in VGPRs: the write
 // toggle and pad strobe as `flags` bits, pad 1's buttons in `flags` bits
-// 8-15, and `io` = open bus (bits 0-7) | PPUSTATUS (8-15) | pad 1 shift
-// register (16-23) | pad 1 reads (24-27) | pad 2 reads (28-31).
+// 8-15, the OAM byte at OAMADDR (what a `$2004` read returns) in `flags`
+// bits 16-23, and `io` = open bus (bits 0-7) | PPUSTATUS (8-15) | pad 1
+// shift register (16-23) | pad 1 reads (24-27) | pad 2 reads (28-31).
 constexpr std::uint32_t kWToggle = 16, kStrobeBit = 32;
 
 // Row of the interleaved RAM/PRG-RAM array that lanes with nothing to store
@@ -204,6 +205,11 @@ struct Console {
     }
     __device__ __forceinline__ void set_c2_count(std::uint32_t n) { io = (io & 0x0FFFFFFFu) | (n << 28); }
     __device__ __forceinline__ std::uint32_t buttons() const { return ubfe(flags, 8, 8); }
+    // OAM and OAMADDR change only in the rare work (`$2003`/`$2004` writes,
+    // OAM DMA) and between launches, so the byte a `$2004` read returns
+    // (ppu.hpp:88-89: no side effects) is kept up to date there.
+    __device__ __forceinline__ std::uint32_t oam_data() const { return ubfe(flags, 16, 8); }
+    __device__ __forceinline__ void set_oam_data(std::uint32_t v) { flags = (flags & ~0xFF0000u) | ((v & 0xFF) << 16); }
 
     // ---- LDS register area ----------------------------------------------------------
     __device__ __forceinline__ std::uint32_t r8(std::uint32_t f) const { return lds[base + kRegs + f]; }
@@ -320,7 +326,7 @@ struct Console {
                 flags &= ~(kNmiPending | kWToggle);
                 return val;
             }
-            if (reg == 4) return vmem()[vram::kOam + r8(reg::kOamAddr)];
+            if (reg == 4) return oam_data();
             if (reg == 7) {
                 const std::uint32_t v = r16(reg::kV);
                 const std::uint32_t va = v & 0x3FFF;
@@ -373,10 +379,12 @@ struct Console {
             w8(reg::kMask, val);
         } else if (r == 3) {
             w8(reg::kOamAddr, val);
+            set_oam_data(vmem()[vram::kOam + (val & 0xFF)]);
         } else if (r == 4) {
             const std::uint32_t oa = r8(reg::kOamAddr);
             vmem()[vram::kOam + oa] = static_cast<std::uint8_t>(val);
             w8(reg::kOamAddr, oa + 1);
+            set_oam_data(vmem()[vram::kOam + ((oa + 1) & 0xFF)]);
         } else if (r == 5) {
             const std::uint32_t t = r16(reg::kT);
             if (!(flags & kWToggle)) {
@@ -662,6 +670,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         c.p = s.p[env];
         c.flags = (s.nmi_pending[env] ? kNmiPending : 0u) | (s.fault[env] ? kFault : 0u) | (s.w[env] ? kWToggle : 0u) |
                   (strobe ? kStrobeBit : 0u) | (buttons << 8);
+        c.set_oam_data(c.vmem()[vram::kOam + s.oam_addr[env]]);
         c.w32(reg::kFramesLeft, (c.flags & kFault) ? 0u : frameskip);
         c.w32(reg::kFrames, 0);
         c.w32(reg::kBudgetHits, 0);
@@ -1122,16 +1131,23 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
                     for (std::uint32_t k = 0; k < 4; ++k)
                         e_oam[(oa + 4 * lane + k) & 0xFF] = static_cast<std::uint8_t>(val[k]);
                 }
+                // OAM[OAMADDR] is now the page's first byte, lane 0's first.
+                const std::uint32_t first = __builtin_amdgcn_readlane(val[0], 0);
+                if (lane == src) c.set_oam_data(first);
             } else if (lane == src) {
                 // OAMADDR advances with every byte (ppu.hpp:131-134), which a
                 // $2004 read inside the copy observes; it wraps back to `oa`.
+                std::uint32_t first = 0;
                 for (std::uint32_t i = 0; i < 256; ++i) {
                     const std::uint32_t at = (oa + i) & 0xFF;
                     c.w8(reg::kOamAddr, at);
+                    c.set_oam_data(e_oam[at]);   // what a $2004 read in the page returns now
                     const std::uint32_t val = c.bus_rd((page << 8) | i);
                     e_oam[at] = static_cast<std::uint8_t>(val);
+                    if (i == 0) first = val;
                 }
                 c.w8(reg::kOamAddr, oa);
+                c.set_oam_data(first);
             }
         }
         c.flags &= ~kDmaPending;
