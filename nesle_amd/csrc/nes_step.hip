@@ -1099,6 +1099,34 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         std::uint64_t req = __ballot((c.flags & kDmaPending) != 0);
         if constexpr (kStats == 3) cz.v[census::kDma] += req != 0 ? 1u : 0u;
+        if constexpr (!kFull) {
+            // Split layout: the vblank rendezvous starts a wave's NMI handlers,
+            // and with them their DMAs, in the same iteration.  When eight or
+            // more consoles copy pages that live in HBM rows (RAM outside the
+            // LDS rows, PRG RAM), each lane copies its own console's page: a
+            // row's byte for 64 consoles is one coalesced load.
+            const bool dma = (c.flags & kDmaPending) != 0;
+            const std::uint32_t page = lds[c.base + C::kRegs + reg::kDmaPage];
+            const bool hbm_page = (page < 0x20 && (page & 7) >= 2) || (page >= 0x60 && page < 0x80);
+            if (__popcll(req) >= 8 && __builtin_amdgcn_ballot_w64(dma && !hbm_page) == 0) {
+                if (dma) {
+                    const std::uint32_t row0 = page < 0x20 ? ((page & 7) << 8) : ((page << 8) - 0x5800);
+                    const std::uint32_t oa = c.r8(reg::kOamAddr);
+                    std::uint8_t* oam = c.vmem() + vram::kOam;
+                    std::uint32_t first = 0;
+                    for (std::uint32_t i = 0; i < 256; i += 16) {   // 16 loads in flight
+                        std::uint32_t v[16];
+#pragma unroll
+                        for (std::uint32_t k = 0; k < 16; ++k) v[k] = s.ram[c.goff(row0 + i + k)];
+#pragma unroll
+                        for (std::uint32_t k = 0; k < 16; ++k) oam[(oa + i + k) & 0xFF] = static_cast<std::uint8_t>(v[k]);
+                        if (i == 0) first = v[0];
+                    }
+                    c.set_oam_data(first);   // OAM[OAMADDR] is now the page's first byte
+                }
+                req = 0;
+            }
+        }
         while (req != 0) {
             const std::uint32_t src = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(req)) - 1);
             req &= req - 1;
