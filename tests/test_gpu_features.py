@@ -126,3 +126,74 @@ def test_rare_paths_match_oracle(num_envs):
                     assert got[O.OFF["fault"]] & 1
                 assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
     assert stopped and len(stopped) < len(sample) and deep and wrapped
+
+
+def oam_rom() -> bytes:
+    """OAMADDR and OAMDATA traffic in every order: `$2003` writes, `$2004`
+    reads before and after `$2004` writes, and an OAM DMA every frame from a
+    page that cycles through HBM-row RAM ($05), LDS-resident RAM ($00), PRG
+    RAM ($61) and the PPU registers ($20, read through the bus with their side
+    effects), each followed by a `$2004` read.  Every value read lands in RAM."""
+    a = _Asm()
+    a.org(0x8000)
+    a.op("SEI"); a.op("CLD"); a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)   # NMI on
+    a.op("LDA", "imm", 0x1E); a.op("STA", "abs", 0x2001)
+    a.label("MAIN")
+    a.op("INC", "zp", 0x20); a.op("LDX", "zp", 0x20)
+    a.op("TXA"); a.op("STA", "absx", 0x0500); a.op("STA", "absx", 0x6100)   # DMA source pages
+    a.op("LDA", "zp", 0x10); a.op("EOR", "zp", 0x20); a.op("STA", "abs", 0x2003)
+    a.op("LDA", "abs", 0x2004); a.op("STA", "absx", 0x0300)                # OAM[OAMADDR]
+    a.op("TXA"); a.op("EOR", "imm", 0xA5); a.op("STA", "abs", 0x2004)       # write, OAMADDR + 1
+    a.op("LDA", "abs", 0x2004); a.op("STA", "absx", 0x0400)                # the next byte
+    a.op("LDA", "zp", 0x10); a.op("AND", "imm", 0x03); a.op("BNE", "rel", "MAIN")
+    a.op("LDA", "abs", 0x2004); a.op("STA", "absx", 0x0700)
+    a.op("JMP", "abs", "MAIN")
+    a.org(0x9000)                               # NMI: read pad 1, DMA from the next page, read OAMDATA
+    a.op("PHA"); a.op("TXA"); a.op("PHA")
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016); a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDX", "imm", 8)
+    rd = a.label()
+    a.op("LDA", "abs", 0x4016); a.op("LSR", "acc"); a.op("ROL", "zp", 0x10); a.op("DEX"); a.op("BNE", "rel", rd)
+    a.op("INC", "zp", 0x11)
+    a.op("LDA", "zp", 0x11); a.op("AND", "imm", 3); a.op("TAX"); a.op("LDA", "absx", 0x9100)
+    a.op("STA", "abs", 0x4014)
+    a.op("LDX", "zp", 0x11); a.op("LDA", "abs", 0x2004); a.op("STA", "absx", 0x0600)
+    a.op("PLA"); a.op("TAX"); a.op("PLA"); a.op("RTI")
+    a.org(0x9100)
+    a.byte(0x05, 0x00, 0x61, 0x20)
+    a.resolve()
+    prg = bytearray(a.prg)
+    for at, v in ((0xFFFA, 0x9000), (0xFFFC, 0x8000), (0xFFFE, 0x8000)):
+        prg[at - 0x8000] = v & 0xFF
+        prg[at - 0x8000 + 1] = v >> 8
+    chr_rom = bytes((i * 53 + 7) & 0xFF for i in range(0x2000))
+    return bytes(b"NES\x1a" + bytes([2, 1, 0x01, 0]) + bytes(8)) + bytes(prg) + chr_rom
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_oam_data_reads_match_oracle(num_envs):
+    """The step kernel keeps the OAM byte at OAMADDR in a register, refreshed
+    by `$2003`/`$2004` writes, by OAM DMA (whole-wave, lane-parallel and
+    through-the-bus copies) and when a launch loads its state; every `$2004`
+    read of this ROM is stored in RAM, and RAM, OAM and OAMADDR are compared
+    with the oracle after every step."""
+    rom = oam_rom()
+    steps = 10
+    sample = list(range(64)) if num_envs == 64 else sorted({0, 1, 31, 63, 64, 4095, 8191, 12000, num_envs - 1,
+                                                             *np.random.default_rng(11).integers(0, num_envs, 8)})
+    say(f"[gpu] OAM data reads: N={num_envs} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    cons = {e: O.Oracle(rom) for e in sample}
+    for c in cons.values():
+        c.set_reward()
+    for k in range(steps):
+        m = masks_for(911, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins = b.host(abi.VIEW_INSTRUCTIONS)
+        for e, c in cons.items():
+            n, _, _ = c.step(int(m[e]), 4)
+            assert ins[e] == n, f"step {k} env {e}"
+            got, ref = b.save_state(e), c.save()
+            assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
