@@ -881,18 +881,19 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         const std::uint32_t carry = sel(d19, xa, sum >> 8) & 1;
         const std::uint32_t ovf = ((~(xa ^ xb) & (xa ^ sum)) >> 1) & 0x40;
         const std::uint32_t nv_bit = M & 0xC0, nv_alu = (r & 0x80) | ovf;
+        // Z by bit arithmetic (r is a byte, so ((r - 1) >> 30) & 2 is 2 exactly
+        // when r is 0): a compare and a select on the fresh compare result
+        // cost the wave a hazard stall (`s_nop`).  With all RAM in LDS the
+        // N/V choice too; the split layout measured 0.6 % slower with it and
+        // keeps that select.
         std::uint32_t f;
         if constexpr (kFull) {
-            // N/V and Z by bit arithmetic: a compare and a select on the fresh
-            // compare result cost the wave two hazard stalls (`s_nop`) here.
-            // The split layout measured 0.9 % slower this way and keeps the
-            // selects.
             std::uint32_t nvm = static_cast<std::uint32_t>(static_cast<std::int32_t>(d0 << 8) >> 31);
             asm("" : "+v"(nvm));   // keeps the mask a bitwise select
-            f = sel(nvm, nv_bit, nv_alu) | (((r - 1u) >> 30) & 2u) | carry;   // r is a byte: Z when it is 0
+            f = sel(nvm, nv_bit, nv_alu) | (((r - 1u) >> 30) & 2u) | carry;
         } else {
             const std::uint32_t nv = (d0 & 0x800000) ? nv_bit : nv_alu;
-            f = nv | (r == 0 ? 2u : 0u) | carry;
+            f = nv | (((r - 1u) >> 30) & 2u) | carry;
         }
         const std::uint32_t fm = d0 >> 24;
         const std::uint32_t p1 = (p0 & ~fm) | (f & fm);
