@@ -27,9 +27,9 @@
 //    branch-free datapath (addressing, stack window, next PC, ALU, flags).
 //    Finished lanes and NMI entry run as virtual opcodes, so nothing needs a
 //    commit select.  The registers that I/O reads touch ($2002, $4016/7:
-//    status, open bus, write toggle, pads) are packed into VGPRs, so those
-//    reads take no LDS round trip; the other PPU registers live in a
-//    per-console LDS area.
+//    status, open bus, write toggle, pads; for $2004 the OAM byte at
+//    OAMADDR) are packed into VGPRs, so those reads take no memory round
+//    trip; the other PPU registers live in a per-console LDS area.
 //  * With RAM split between LDS and HBM, the next instruction is decoded one
 //    iteration ahead: its effective address is computed and its HBM operand
 //    load issued at the end of the current iteration, so the load has a
@@ -39,8 +39,15 @@
 //    reads by selects, the rest behind a branch); everything rare (I/O
 //    writes, JMP indirect, stack wrap, idle loops, illegal opcodes, PPU
 //    events, OAM DMA, code outside ROM) sits behind one wave-uniform test.
-//  * OAM DMA is done by the whole wave for one console at a time (4 bytes per
-//    lane) instead of a 256-iteration loop in one lane.
+//  * With RAM split, a console that reaches vblank waits for the rest of its
+//    wave (the vblank rendezvous), so the NMI handlers, which hold the I/O
+//    writes, OAM DMA and the frame capture, run in step and share rare-path
+//    entries.  OAM DMA and the capture are then copied by each lane for its
+//    own console; otherwise the whole wave copies one console at a time
+//    instead of a 256-iteration loop in one lane.
+//  * The launch state's fields that only the rare work and the write-back
+//    read come through a reloaded pointer to the kernel arguments (`reload`),
+//    so the loop's scalar registers stay with its constants.
 //  * The CPU cycle counter is not updated per instruction: every cycle is 3
 //    PPU dots, so cycles advance by (dots advanced) / 3 at the end.
 #include <hip/hip_runtime.h>
