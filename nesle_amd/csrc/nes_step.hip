@@ -160,10 +160,14 @@ __device__ __forceinline__ std::uint32_t ubfe(std::uint32_t v, std::uint32_t off
 
 // Dots from `fd` to the next timing event: sprite-0 dot, vblank, pre-render
 // line, frame end (ppu.hpp:19-25,136-147).  Signed differences keep every
-// candidate comparison a plain select.
-__device__ __forceinline__ std::uint32_t to_event(std::uint32_t fd) {
+// candidate comparison a plain select.  `through`: the frame end changes
+// nothing a program can observe (the frame count and the dot counter's wrap,
+// which settle() applies when it crosses it), so when it is not the launch's
+// last, the countdown runs on to the next frame's sprite-0 dot, one rare-work
+// entry per frame fewer.
+__device__ __forceinline__ std::uint32_t to_event(std::uint32_t fd, bool through) {
     const std::int32_t c = static_cast<std::int32_t>(fd);
-    std::int32_t d = static_cast<std::int32_t>(kFrameDots) - c;
+    std::int32_t d = static_cast<std::int32_t>(through ? kFrameDots + kSprite0Dot : kFrameDots) - c;
     const std::int32_t s0 = static_cast<std::int32_t>(kSprite0Dot) - c;
     const std::int32_t vb = static_cast<std::int32_t>(kVblankDot) - c;
     const std::int32_t pr = static_cast<std::int32_t>(kPreRenderDot) - c;
@@ -644,6 +648,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     C c{(KState*)__builtin_amdgcn_kernarg_segment_ptr(), mine ? env : 0u, base, P};
     if constexpr (!kFull) c.vm = s.vram + static_cast<std::size_t>(c.env) * s.vram_stride;
     std::uint32_t fd0 = 0, horizon0 = 0;
+    // The countdown may run through a frame end (to_event) unless the frame
+    // budget can bind: the frame's instruction count then starts again only at
+    // the next event, at most 1,762 instructions later (10,571 dots at six or
+    // more per instruction), so a budget of 32,768 or more never binds early.
+    const bool through_ok = !kBudget || max_instr >= 32768;
     if (mine) {
         // This console's RAM rows that live in LDS.
         const std::uint8_t* g = s.ram + env;
@@ -665,7 +674,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         c.w8(reg::kScrollX, s.scroll_x[env]); c.w8(reg::kScrollY, s.scroll_y[env]);
         c.w16(reg::kV, s.v[env]); c.w16(reg::kT, s.t[env]);
         fd0 = s.frame_dot[env];
-        horizon0 = to_event(fd0);
+        horizon0 = to_event(fd0, frameskip > 1 && through_ok);
         c.w32(reg::kFrameDot, fd0);
         c.w32(reg::kHorizon, horizon0);
         // The pad reads this step's mask; a high strobe re-latches (controller.hpp:20-25).
@@ -1062,16 +1071,17 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         bool at_vblank = false;
         if (counted && left <= 0) {  // a timing event was crossed: settle the PPU
             const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), kBudget, &at_vblank);
-            const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
-            c.w32(reg::kHorizon, h);
-            left = static_cast<std::int32_t>(h);
+            std::uint32_t fl = c.r32(reg::kFramesLeft);
             if (fc) {
                 c.w32(reg::kFrames, c.r32(reg::kFrames) + 1);
                 in_frame = 0;
-                const std::uint32_t fl = c.r32(reg::kFramesLeft) - 1;
+                fl -= 1;
                 c.w32(reg::kFramesLeft, fl);
                 if (fl == 0) active = false;
             }
+            const std::uint32_t h = to_event(c.r32(reg::kFrameDot), fl > 1 && through_ok);
+            c.w32(reg::kHorizon, h);
+            left = static_cast<std::int32_t>(h);
         }
         if constexpr (!kFull) {
             // Vblank rendezvous: a console that has just reached vblank waits
@@ -1097,7 +1107,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         }
         if (kBudget && counted && active && in_frame >= max_instr) {  // per-frame budget (cuda_module.cu:1467)
             const std::uint32_t fc = c.settle(c.r32(reg::kHorizon) - static_cast<std::uint32_t>(left), true);
-            const std::uint32_t h = to_event(c.r32(reg::kFrameDot));
+            const std::uint32_t h = to_event(c.r32(reg::kFrameDot), false);
             c.w32(reg::kHorizon, h);
             left = static_cast<std::int32_t>(h);
             c.w32(reg::kFrames, c.r32(reg::kFrames) + fc);
