@@ -919,7 +919,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // Memory writes: the stack window (pushed or old bytes), then the
         // operand to LDS (non-writers store to their spare byte).
         {   // one unaligned 4-byte write: the window bytes and SP+1 as read
-            const std::uint32_t win4 = (win & 0xFFFFFFu) | (w1 << 24);
+            std::uint32_t win4 = (win & 0xFFFFFFu) | (w1 << 24);
+            // All RAM in LDS: a push that wraps below $0100 is the stack side
+            // path's, and the window's first bytes then lie in the zero page
+            // ($00FE-$00FF): they get back what was read.  (The split layout
+            // moves the window to the spare bytes before it can leave page 1.)
+            if constexpr (kFull) win4 = stack_side ? wlo : win4;
             __builtin_memcpy(lds + wb, &win4, 4);
         }
         const std::uint32_t waddr = (wr && ram_lds) ? ram_a : spare;

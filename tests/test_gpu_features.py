@@ -197,3 +197,67 @@ def test_oam_data_reads_match_oracle(num_envs):
             assert ins[e] == n, f"step {k} env {e}"
             got, ref = b.save_state(e), c.save()
             assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+
+
+def stack_wrap_rom() -> bytes:
+    """The stack pointer at both ends of page 1: JSR/RTS, PHA/PLA, PHP/PLP and
+    the NMI's pushes with SP at $00-$07 (pushes wrap from $0100 to $01FF) and
+    pulls with SP at $FE/$FF (pulls wrap from $01FF to $0100), so the
+    six-byte stack window the step kernel reads wraps around the page."""
+    a = _Asm()
+    a.org(0x8000)
+    a.op("SEI"); a.op("CLD"); a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)   # NMI on
+    a.label("MAIN")
+    a.op("INC", "zp", 0x20); a.op("LDA", "zp", 0x20); a.op("AND", "imm", 0x07); a.op("TAX"); a.op("TXS")
+    a.op("JSR", "abs", "SUB")
+    a.op("LDA", "zp", 0x10); a.op("PHA"); a.op("PHP"); a.op("EOR", "imm", 0xFF); a.op("PLP"); a.op("PLA")
+    a.op("STA", "zp", 0x22)
+    a.op("TSX"); a.op("STX", "zp", 0x23)
+    a.op("LDX", "imm", 0xFE); a.op("TXS"); a.op("PLA"); a.op("STA", "zp", 0x24); a.op("PLA"); a.op("STA", "zp", 0x25)
+    a.op("LDA", "zp", 0x20); a.op("PHA"); a.op("PHA"); a.op("TSX"); a.op("STX", "zp", 0x26)
+    a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("JMP", "abs", "MAIN")
+    a.label("SUB")
+    a.op("LDA", "zp", 0x10); a.op("EOR", "imm", 0x5A); a.op("STA", "zp", 0x21); a.op("PHA"); a.op("PLA"); a.op("RTS")
+    a.org(0x9000)                               # NMI: read pad 1 into $10 (pushes wherever SP is)
+    a.op("PHA"); a.op("TXA"); a.op("PHA")
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016); a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDX", "imm", 8)
+    rd = a.label()
+    a.op("LDA", "abs", 0x4016); a.op("LSR", "acc"); a.op("ROL", "zp", 0x10); a.op("DEX"); a.op("BNE", "rel", rd)
+    a.op("INC", "zp", 0x11)
+    a.op("PLA"); a.op("TAX"); a.op("PLA"); a.op("RTI")
+    a.resolve()
+    prg = bytearray(a.prg)
+    for at, v in ((0xFFFA, 0x9000), (0xFFFC, 0x8000), (0xFFFE, 0x8000)):
+        prg[at - 0x8000] = v & 0xFF
+        prg[at - 0x8000 + 1] = v >> 8
+    chr_rom = bytes((i * 29 + 3) & 0xFF for i in range(0x2000))
+    return bytes(b"NES\x1a" + bytes([2, 1, 0x01, 0]) + bytes(8)) + bytes(prg) + chr_rom
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_stack_wrap_matches_oracle(num_envs):
+    """Stack accesses that wrap around page 1 (the step kernel's stack window
+    then goes through its rare path in both LDS layouts), compared with the
+    oracle after every step: instruction counts and whole console states."""
+    rom = stack_wrap_rom()
+    steps = 8
+    sample = list(range(64)) if num_envs == 64 else sorted({0, 1, 31, 63, 64, 4095, 8191, 12000, num_envs - 1,
+                                                             *np.random.default_rng(13).integers(0, num_envs, 8)})
+    say(f"[gpu] stack wrap: N={num_envs} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    cons = {e: O.Oracle(rom) for e in sample}
+    for c in cons.values():
+        c.set_reward()
+    for k in range(steps):
+        m = masks_for(913, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins = b.host(abi.VIEW_INSTRUCTIONS)
+        for e, c in cons.items():
+            n, _, _ = c.step(int(m[e]), 4)
+            assert ins[e] == n, f"step {k} env {e}"
+            got, ref = b.save_state(e), c.save()
+            assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
