@@ -261,3 +261,86 @@ def test_stack_wrap_matches_oracle(num_envs):
             assert ins[e] == n, f"step {k} env {e}"
             got, ref = b.save_state(e), c.save()
             assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+
+
+def io_corner_rom() -> bytes:
+    """I/O register paths the benchmark ROM never takes: pad 2 reads, `$4015`
+    written and read, palette writes and reads through `$2006/$2007`
+    (including the `$3F10` mirror and the buffer fill a palette read does),
+    `$2007` with the 32-byte increment, `$2002` reads between `$2005` writes
+    (the write toggle), reads of `$4016` with the strobe held high, and NMI
+    switched off and on again during vblank (an immediate NMI).  Every value
+    read is stored in RAM."""
+    a = _Asm()
+    a.org(0x8000)
+    a.op("SEI"); a.op("CLD"); a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)
+    a.label("MAIN")
+    a.op("INC", "zp", 0x20); a.op("LDA", "zp", 0x20); a.op("AND", "imm", 0x0F); a.op("TAX")
+    a.op("LDA", "abs", 0x4017); a.op("STA", "absx", 0x0300); a.op("LDA", "abs", 0x4017); a.op("STA", "absx", 0x0310)
+    a.op("LDA", "zp", 0x20); a.op("STA", "abs", 0x4015); a.op("LDA", "abs", 0x4015); a.op("STA", "absx", 0x0320)
+    a.op("LDA", "imm", 0x3F); a.op("STA", "abs", 0x2006); a.op("LDA", "imm", 0x10); a.op("STA", "abs", 0x2006)
+    a.op("LDA", "zp", 0x20); a.op("STA", "abs", 0x2007)                        # $3F10 -> $3F00
+    a.op("LDA", "imm", 0x3F); a.op("STA", "abs", 0x2006); a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x2006)
+    a.op("LDA", "abs", 0x2007); a.op("STA", "absx", 0x0330)                     # palette read, buffer fill
+    a.op("LDA", "abs", 0x2007); a.op("STA", "absx", 0x0340)
+    a.op("LDA", "imm", 0x84); a.op("STA", "abs", 0x2000)                        # +32 per $2007 access
+    a.op("LDA", "imm", 0x20); a.op("STA", "abs", 0x2006); a.op("STX", "abs", 0x2006)
+    a.op("LDA", "zp", 0x10); a.op("STA", "abs", 0x2007); a.op("EOR", "imm", 0xFF); a.op("STA", "abs", 0x2007)
+    a.op("LDA", "imm", 0x20); a.op("STA", "abs", 0x2006); a.op("STX", "abs", 0x2006)
+    a.op("LDA", "abs", 0x2007); a.op("LDA", "abs", 0x2007); a.op("STA", "absx", 0x0350)
+    a.op("LDA", "abs", 0x2007); a.op("STA", "absx", 0x0360)
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)
+    a.op("LDA", "zp", 0x20); a.op("STA", "abs", 0x2005); a.op("LDA", "abs", 0x2002); a.op("STA", "absx", 0x0370)
+    a.op("LDA", "zp", 0x10); a.op("STA", "abs", 0x2005); a.op("STA", "abs", 0x2005)
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016)                          # strobe held high
+    a.op("LDA", "abs", 0x4016); a.op("STA", "absx", 0x0380); a.op("LDA", "abs", 0x4016); a.op("STA", "absx", 0x0390)
+    a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDA", "abs", 0x4016); a.op("STA", "absx", 0x03A0)
+    a.op("LDA", "imm", 0x00); a.op("STA", "abs", 0x2000)                       # NMI off, then on again:
+    a.op("LDA", "zp", 0x20); a.op("AND", "imm", 0x03); a.op("BEQ", "rel", "skip")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)                       # in vblank -> NMI at once
+    a.label("skip")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)
+    a.op("JMP", "abs", "MAIN")
+    a.org(0x9000)                               # NMI: read pad 1 into $10, count, read PPUSTATUS
+    a.op("PHA"); a.op("TXA"); a.op("PHA")
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016); a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDX", "imm", 8)
+    rd = a.label()
+    a.op("LDA", "abs", 0x4016); a.op("LSR", "acc"); a.op("ROL", "zp", 0x10); a.op("DEX"); a.op("BNE", "rel", rd)
+    a.op("INC", "zp", 0x11); a.op("LDX", "zp", 0x11); a.op("LDA", "abs", 0x2002); a.op("STA", "absx", 0x0400)
+    a.op("PLA"); a.op("TAX"); a.op("PLA"); a.op("RTI")
+    a.resolve()
+    prg = bytearray(a.prg)
+    for at, v in ((0xFFFA, 0x9000), (0xFFFC, 0x8000), (0xFFFE, 0x8000)):
+        prg[at - 0x8000] = v & 0xFF
+        prg[at - 0x8000 + 1] = v >> 8
+    chr_rom = bytes((i * 41 + 5) & 0xFF for i in range(0x2000))
+    return bytes(b"NES\x1a" + bytes([2, 1, 0x01, 0]) + bytes(8)) + bytes(prg) + chr_rom
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_io_corner_cases_match_oracle(num_envs):
+    """The I/O register paths of `io_corner_rom`, compared with the oracle
+    after every step: instruction counts and whole console states (RAM with
+    every value read, PPU registers, palette, nametables, pads)."""
+    rom = io_corner_rom()
+    steps = 8
+    sample = list(range(64)) if num_envs == 64 else sorted({0, 1, 31, 63, 64, 4095, 8191, 12000, num_envs - 1,
+                                                             *np.random.default_rng(17).integers(0, num_envs, 8)})
+    say(f"[gpu] I/O corner cases: N={num_envs} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    cons = {e: O.Oracle(rom) for e in sample}
+    for c in cons.values():
+        c.set_reward()
+    for k in range(steps):
+        m = masks_for(917, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins = b.host(abi.VIEW_INSTRUCTIONS)
+        for e, c in cons.items():
+            n, _, _ = c.step(int(m[e]), 4)
+            assert ins[e] == n, f"step {k} env {e}"
+            got, ref = b.save_state(e), c.save()
+            assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
