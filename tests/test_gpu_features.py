@@ -344,3 +344,67 @@ def test_io_corner_cases_match_oracle(num_envs):
             assert ins[e] == n, f"step {k} env {e}"
             got, ref = b.save_state(e), c.save()
             assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
+
+
+def address_wrap_rom() -> bytes:
+    """Effective addresses that wrap: a `(zp),Y` pointer at $FF/$00, `(zp,X)`
+    pointers whose zero-page address wraps past $FF, `abs,X` and `abs,Y` past
+    $FFFF into RAM (loads and stores), and `zp,X` past $FF, with pad-dependent
+    index values; every value loaded is stored in RAM."""
+    a = _Asm()
+    a.org(0x8000)
+    a.op("SEI"); a.op("CLD"); a.op("LDX", "imm", 0xFF); a.op("TXS")
+    a.op("LDA", "imm", 0x80); a.op("STA", "abs", 0x2000)
+    a.label("MAIN")
+    a.op("INC", "zp", 0x20)
+    a.op("LDA", "zp", 0x20); a.op("STA", "zp", 0xFF); a.op("LDA", "imm", 0x03); a.op("STA", "zp", 0x00)  # ($FF) -> $03xx
+    a.op("LDY", "zp", 0x10); a.op("LDA", "indy", 0xFF); a.op("STA", "zp", 0x30)
+    a.op("LDA", "zp", 0x20); a.op("STA", "indy", 0xFF)
+    a.op("LDX", "imm", 0x01); a.op("LDA", "indx", 0xFE); a.op("STA", "zp", 0x31)   # ($FE,X) -> pointer at $FF/$00
+    a.op("LDX", "zp", 0x10); a.op("LDA", "indx", 0xF0); a.op("STA", "zp", 0x32)   # ($F0+X) wraps for X >= $10
+    a.op("LDA", "absx", 0xFFF0); a.op("STA", "zp", 0x33)                           # $FFF0+X past $FFFF
+    a.op("LDA", "zp", 0x20); a.op("STA", "absx", 0xFFF0)                           # store into RAM $00xx
+    a.op("LDY", "zp", 0x20); a.op("LDA", "absy", 0xFF80); a.op("STA", "zp", 0x34)
+    a.op("LDA", "zpx", 0xC0); a.op("STA", "zp", 0x35)                              # $C0+X wraps in page 0
+    a.op("LDA", "zp", 0x11); a.op("STA", "zpx", 0xE0)
+    a.op("JMP", "abs", "MAIN")
+    a.org(0x9000)
+    a.op("PHA"); a.op("TXA"); a.op("PHA")
+    a.op("LDA", "imm", 1); a.op("STA", "abs", 0x4016); a.op("LDA", "imm", 0); a.op("STA", "abs", 0x4016)
+    a.op("LDX", "imm", 8)
+    rd = a.label()
+    a.op("LDA", "abs", 0x4016); a.op("LSR", "acc"); a.op("ROL", "zp", 0x10); a.op("DEX"); a.op("BNE", "rel", rd)
+    a.op("INC", "zp", 0x11)
+    a.op("PLA"); a.op("TAX"); a.op("PLA"); a.op("RTI")
+    a.resolve()
+    prg = bytearray(a.prg)
+    for at, v in ((0xFFFA, 0x9000), (0xFFFC, 0x8000), (0xFFFE, 0x8000)):
+        prg[at - 0x8000] = v & 0xFF
+        prg[at - 0x8000 + 1] = v >> 8
+    chr_rom = bytes((i * 23 + 9) & 0xFF for i in range(0x2000))
+    return bytes(b"NES\x1a" + bytes([2, 1, 0x01, 0]) + bytes(8)) + bytes(prg) + chr_rom
+
+
+@pytest.mark.parametrize("num_envs", [64, 16384])
+def test_address_wrap_matches_oracle(num_envs):
+    """Wrapping effective addresses of `address_wrap_rom`, compared with the
+    oracle after every step: instruction counts and whole console states."""
+    rom = address_wrap_rom()
+    steps = 6
+    sample = list(range(64)) if num_envs == 64 else sorted({0, 1, 31, 63, 64, 4095, 8191, 12000, num_envs - 1,
+                                                             *np.random.default_rng(19).integers(0, num_envs, 8)})
+    say(f"[gpu] address wrap: N={num_envs} fs=4 steps={steps} sample={len(sample)}")
+    b = abi.Batch(rom, num_envs, frameskip=4)
+    cons = {e: O.Oracle(rom) for e in sample}
+    for c in cons.values():
+        c.set_reward()
+    for k in range(steps):
+        m = masks_for(919, num_envs, k)
+        b.set_actions(m)
+        b.step(stats_mode=1)
+        ins = b.host(abi.VIEW_INSTRUCTIONS)
+        for e, c in cons.items():
+            n, _, _ = c.step(int(m[e]), 4)
+            assert ins[e] == n, f"step {k} env {e}"
+            got, ref = b.save_state(e), c.save()
+            assert np.array_equal(got, ref), f"step {k} env {e}: {first_diff(got, ref)}"
