@@ -770,9 +770,19 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     auto address = [&](std::uint32_t o, std::uint32_t lo, std::uint32_t hi, std::uint32_t regs) {
         address_at(zp_pointer(o, lo, regs), lo, hi, regs);
     };
+    // Split layout: the decode also leaves the next iteration's microcode
+    // row (offset in the slice tables) and stack-window address, so the loop
+    // top issues its LDS reads without computing their addresses first.
+    [[maybe_unused]] std::uint32_t mwo_c = 0, wb_c = 0;
+    auto window_at = [&](std::uint32_t regs) {
+        const std::uint32_t sp = regs >> 24;
+        return sp >= 0x82u ? base + C::kStk + sp : spare;   // below $0180 (not in LDS): the spare bytes
+    };
     if constexpr (!kFull) {
         slices(active ? op : mc::kNopEntry);
         address(op, b1, b2, c.regs);
+        mwo_c = 16 * (active ? op : mc::kNopEntry);
+        wb_c = window_at(c.regs);
     }
     [[maybe_unused]] WaveCensus cz;
     [[maybe_unused]] std::uint64_t t_loop = 0, t_rare = 0;
@@ -785,7 +795,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     if (__builtin_amdgcn_ballot_w64(active) != 0) for (;;) {
         const std::uint32_t pc0 = c.pc, regs0 = c.regs, p0 = c.p;
         const std::uint32_t mi = active ? op : mc::kNopEntry;
-        const std::uint8_t* mw = lds + kLdsMicro + 16 * mi;
+        const std::uint8_t* mw = lds + kLdsMicro + (kFull ? 16 * mi : mwo_c);
         if constexpr (kFull) {
             slices(mi);
             address(op, b1, b2, regs0);
@@ -804,7 +814,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // in the LDS half of the page, else a harmless spare area).
         const std::uint32_t sp = regs0 >> 24;
         std::uint32_t wb = base + C::kStk + sp;
-        if (!kFull) wb = sp >= 0x82u ? wb : spare;
+        if (!kFull) wb = wb_c;
         // One unaligned 8-byte read; the last two bytes, unused, lie inside
         // the console's block (or its spare and register bytes).
         std::uint64_t wq;
@@ -945,7 +955,9 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             ptr_n = zp_pointer(op_n, b1_n, regs_n);
             // Slices 0 and 4 of the next instruction's microcode, read
             // together with its pointer.
-            const std::uint8_t* mw_n = lds + kLdsMicro + 16 * (active ? op_n : mc::kNopEntry);
+            mwo_c = 16 * (active ? op_n : mc::kNopEntry);
+            const std::uint8_t* mw_n = lds + kLdsMicro + mwo_c;
+            wb_c = window_at(regs_n);
             ma_n = *reinterpret_cast<const uint4*>(mw_n);
             me_n = *reinterpret_cast<const uint4*>(mw_n + 4 * kMicroQuarter);
         }
@@ -1284,6 +1296,8 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             }
             slices(active ? op : mc::kNopEntry);
             address(op, b1, b2, c.regs);
+            mwo_c = 16 * (active ? op : mc::kNopEntry);
+            wb_c = window_at(c.regs);
             if constexpr (kStats == 3) cz.v[census::kCyclesRedo] += clock64() - t_sub;
         }
         if constexpr (kStats == 3) cz.v[census::kCyclesRare] += clock64() - t_rare;
