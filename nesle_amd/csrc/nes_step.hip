@@ -771,9 +771,12 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         address_at(zp_pointer(o, lo, regs), lo, hi, regs);
     };
     // Split layout: the decode also leaves the next iteration's microcode
-    // row (offset in the slice tables) and stack-window address, so the loop
-    // top issues its LDS reads without computing their addresses first.
+    // row (offset in the slice tables) and stack-window address, and reads
+    // the window itself (after this iteration's LDS writes), so the loop top
+    // issues its LDS reads without computing their addresses first and the
+    // next-PC unit has the window bytes at once.
     [[maybe_unused]] std::uint32_t mwo_c = 0, wb_c = 0;
+    [[maybe_unused]] std::uint64_t wq_c = 0;
     auto window_at = [&](std::uint32_t regs) {
         const std::uint32_t sp = regs >> 24;
         return sp >= 0x82u ? base + C::kStk + sp : spare;   // below $0180 (not in LDS): the spare bytes
@@ -783,6 +786,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         address(op, b1, b2, c.regs);
         mwo_c = 16 * (active ? op : mc::kNopEntry);
         wb_c = window_at(c.regs);
+        __builtin_memcpy(&wq_c, lds + wb_c, 8);
     }
     [[maybe_unused]] WaveCensus cz;
     [[maybe_unused]] std::uint64_t t_loop = 0, t_rare = 0;
@@ -818,7 +822,11 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
         // One unaligned 8-byte read; the last two bytes, unused, lie inside
         // the console's block (or its spare and register bytes).
         std::uint64_t wq;
-        __builtin_memcpy(&wq, lds + wb, 8);
+        if constexpr (kFull) {
+            __builtin_memcpy(&wq, lds + wb, 8);
+        } else {
+            wq = wq_c;   // read by the decode
+        }
         const std::uint32_t wlo = static_cast<std::uint32_t>(wq), whi = static_cast<std::uint32_t>(wq >> 32);
         const std::uint32_t o2 = wlo & 0xFF, o1 = (wlo >> 8) & 0xFF, o0 = (wlo >> 16) & 0xFF;
         const std::uint32_t w1 = wlo >> 24, w2 = whi & 0xFF, w3 = (whi >> 8) & 0xFF;
@@ -958,6 +966,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             mwo_c = 16 * (active ? op_n : mc::kNopEntry);
             const std::uint8_t* mw_n = lds + kLdsMicro + mwo_c;
             wb_c = window_at(regs_n);
+            __builtin_memcpy(&wq_c, lds + wb_c, 8);
             ma_n = *reinterpret_cast<const uint4*>(mw_n);
             me_n = *reinterpret_cast<const uint4*>(mw_n + 4 * kMicroQuarter);
         }
@@ -1298,6 +1307,7 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
             address(op, b1, b2, c.regs);
             mwo_c = 16 * (active ? op : mc::kNopEntry);
             wb_c = window_at(c.regs);
+            __builtin_memcpy(&wq_c, lds + wb_c, 8);
             if constexpr (kStats == 3) cz.v[census::kCyclesRedo] += clock64() - t_sub;
         }
         if constexpr (kStats == 3) cz.v[census::kCyclesRare] += clock64() - t_rare;
