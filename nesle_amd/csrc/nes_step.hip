@@ -1426,13 +1426,20 @@ hipError_t launch_variant(const DeviceState& s, const Geometry& g, std::uint32_t
     return hipGetLastError();
 }
 
-template <int kStats, bool kBudget>
-hipError_t launch_mode(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
-                       hipStream_t stream) {
-    return g.full ? launch_variant<kStats, true, kBudget>(s, g, frameskip, max_instr, stream)
-                  : launch_variant<kStats, false, kBudget>(s, g, frameskip, max_instr, stream);
+// One layout's kernels, for every statistics mode and frame budget.
+template <bool kFull>
+hipError_t launch_layout(const DeviceState& s, const Geometry& g, std::uint32_t frameskip, std::uint32_t max_instr,
+                         int stats_mode, hipStream_t stream) {
+    // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
+    const bool budget = max_instr < 15000;
+    if (stats_mode == 3) return launch_variant<3, kFull, true>(s, g, frameskip, max_instr, stream);
+    if (stats_mode == 2) return launch_variant<2, kFull, true>(s, g, frameskip, max_instr, stream);
+    if (stats_mode == 1) return launch_variant<1, kFull, true>(s, g, frameskip, max_instr, stream);
+    return budget ? launch_variant<0, kFull, true>(s, g, frameskip, max_instr, stream)
+                  : launch_variant<0, kFull, false>(s, g, frameskip, max_instr, stream);
 }
 
+#ifndef NESLE_STEP_FULL_TU
 // Waves per workgroup: NESLE_WAVES_PER_GROUP (4, 8 or 16) overrides the default.
 std::uint32_t waves_per_group() {
     static const std::uint32_t w = [] {
@@ -1442,21 +1449,31 @@ std::uint32_t waves_per_group() {
     }();
     return w;
 }
+#endif
 
 }  // namespace
 
+// The all-RAM-in-LDS kernels are compiled in a translation unit of their own
+// (nes_step_full.hip includes this file with NESLE_STEP_FULL_TU defined), so
+// that they can be built with other scheduler flags than the split layout's.
+hipError_t launch_step_full(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
+                            hipStream_t stream);
+
+#ifdef NESLE_STEP_FULL_TU
+hipError_t launch_step_full(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
+                            hipStream_t stream) {
+    const Geometry g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
+    if (!g.full || g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
+    return launch_layout<true>(s, g, frameskip, max_instr, stats_mode, stream);
+}
+#else
 hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
                        hipStream_t stream) {
-    Geometry g = geometry(s.n, waves_per_group());
-    if (g.full && g.waves != 4) g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
+    const Geometry g = geometry(s.n, waves_per_group());
+    if (g.full) return launch_step_full(s, frameskip, max_instr, stats_mode, stream);
     if (g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
-    // A frame needs at most ceil(89,342 / 6) = 14,891 instructions.
-    const bool budget = max_instr < 15000;
-    if (stats_mode == 3) return launch_mode<3, true>(s, g, frameskip, max_instr, stream);
-    if (stats_mode == 2) return launch_mode<2, true>(s, g, frameskip, max_instr, stream);
-    if (stats_mode == 1) return launch_mode<1, true>(s, g, frameskip, max_instr, stream);
-    return budget ? launch_mode<0, true>(s, g, frameskip, max_instr, stream)
-                  : launch_mode<0, false>(s, g, frameskip, max_instr, stream);
+    return launch_layout<false>(s, g, frameskip, max_instr, stats_mode, stream);
 }
+#endif
 
 }  // namespace nesle

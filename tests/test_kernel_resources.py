@@ -21,8 +21,8 @@ pytestmark = pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not avai
 
 def _kernels(source: Path, tmp_path: Path) -> dict[str, dict[str, int]]:
     out = tmp_path / (source.stem + ".s")
-    flags = [f for f in build.HIP_FLAGS if f not in ("-shared", "-fPIC")]
-    cmd = [HIPCC, "--offload-arch=gfx950", "--offload-device-only", "-S", *flags, "-o", str(out), str(source)]
+    cmd = [HIPCC, "--offload-arch=gfx950", "--offload-device-only", "-S", *build.source_flags(source), "-o", str(out),
+           str(source)]
     subprocess.run(cmd, check=True, capture_output=True, text=True)
     meta = out.read_text().split("amdhsa.kernels:", 1)[1]
     kernels = {}
@@ -44,10 +44,15 @@ def test_render_kernel_lds_fits_five_workgroups(tmp_path):
     assert render[0]["private_segment_fixed_size"] == 0
 
 
-def test_step_kernels_use_no_scratch(tmp_path):
+@pytest.mark.parametrize("source,full", [("nes_step.hip", 0), ("nes_step_full.hip", 1)])
+def test_step_kernels_use_no_scratch(tmp_path, source, full):
     """Every step kernel but the census build (stats mode 3, a measurement
-    variant whose counters may spill) keeps its state in registers and LDS."""
-    kernels = _kernels(build.CSRC / "nes_step.hip", tmp_path)
+    variant whose counters may spill) keeps its state in registers and LDS.
+    The split-layout instances come from nes_step.hip, the all-RAM-in-LDS
+    ones from nes_step_full.hip (its own scheduler flag), each built with the
+    flags the package build gives it."""
+    kernels = _kernels(build.CSRC / source, tmp_path)
     steps = {k: v for k, v in kernels.items() if "step_kernel" in k and "step_kernelILi3E" not in k}
-    assert len(steps) >= 4
+    assert len(steps) == 4
+    assert all(re.search(r"step_kernelILi\dELb(\d)E", k).group(1) == str(full) for k in steps), sorted(steps)
     assert all(v["private_segment_fixed_size"] == 0 for v in steps.values()), steps
