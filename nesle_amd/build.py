@@ -28,8 +28,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libnesle_hip.so"
-HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_step_full.hip", CSRC / "nes_kernels.hip", CSRC / "nes_render.hip",
-               CSRC / "nes_host.hip", CSRC / "ppo_head.hip", CSRC / "smb_shaped.hip"]
+HIP_SOURCES = [CSRC / "nes_step.hip", CSRC / "nes_step_full.hip", CSRC / "nes_step_narrow.hip", CSRC / "nes_kernels.hip",
+               CSRC / "nes_render.hip", CSRC / "nes_host.hip", CSRC / "ppo_head.hip", CSRC / "smb_shaped.hip"]
 SHIM_SOURCE = CSRC / "cuda_core_module.cpp"
 
 HIP_FLAGS = [
@@ -41,11 +41,16 @@ HIP_FLAGS = [
 ]
 
 
-# Flags of one source on top of HIP_FLAGS.  The all-RAM-in-LDS step kernels
-# (nes_step_full.hip) run 2-3 % faster under LLVM's iterative ILP scheduler;
-# the split-layout ones (nes_step.hip) 2.5 % slower, so they keep the default.
+# Flags of one source on top of HIP_FLAGS.  The step kernel's instances come
+# from three translation units, each with the scheduler setting measured
+# fastest for it: all RAM in LDS (nes_step_full.hip, up to 8,192 consoles)
+# LLVM's iterative ILP scheduler, 2-3 % faster; the split layout at 16 or 32
+# consoles per wave (nes_step_narrow.hip) the machine scheduler off, 2-3 %
+# faster; at 64 per wave (nes_step.hip, 65,536 consoles) the default, as both
+# of the others run 0.6-2.5 % slower there.
 SOURCE_FLAGS = {
     CSRC / "nes_step_full.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    CSRC / "nes_step_narrow.hip": ["-mllvm", "-enable-misched=false"],
 }
 
 

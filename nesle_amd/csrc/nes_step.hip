@@ -1393,6 +1393,14 @@ __global__ void __launch_bounds__(kFull ? 256 : kMaxBlock) step_kernel(DeviceSta
     }
 }
 
+// Which of the step kernel's translation units this is (see launch_step).
+#ifndef NESLE_STEP_PART
+#define NESLE_STEP_PART 0
+#endif
+// Split-layout launches with at most 2^5 consoles per wave take the
+// nes_step_narrow.hip instances.
+constexpr std::uint32_t kNarrowLaneBits = 5;
+
 struct Geometry {
     std::uint32_t waves, lane_bits, consoles, blocks, lds;
     bool full;
@@ -1439,7 +1447,7 @@ hipError_t launch_layout(const DeviceState& s, const Geometry& g, std::uint32_t 
                   : launch_variant<0, kFull, false>(s, g, frameskip, max_instr, stream);
 }
 
-#ifndef NESLE_STEP_FULL_TU
+#if NESLE_STEP_PART == 0
 // Waves per workgroup: NESLE_WAVES_PER_GROUP (4, 8 or 16) overrides the default.
 std::uint32_t waves_per_group() {
     static const std::uint32_t w = [] {
@@ -1453,25 +1461,40 @@ std::uint32_t waves_per_group() {
 
 }  // namespace
 
-// The all-RAM-in-LDS kernels are compiled in a translation unit of their own
-// (nes_step_full.hip includes this file with NESLE_STEP_FULL_TU defined), so
-// that they can be built with other scheduler flags than the split layout's.
+// The step kernel's instances come from three translation units, each built
+// with its own scheduler flags (nesle_amd/build.py): this file's own
+// (NESLE_STEP_PART 0: the split layout at 64 consoles per wave, and
+// launch_step), nes_step_full.hip (1: all RAM in LDS) and
+// nes_step_narrow.hip (2: the split layout at 16 or 32 consoles per wave).
+// Each part recomputes the geometry from the console count and waves per
+// workgroup, as launch_step does.
 hipError_t launch_step_full(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
                             hipStream_t stream);
+hipError_t launch_step_narrow(const DeviceState& s, std::uint32_t waves, std::uint32_t frameskip,
+                              std::uint32_t max_instr, int stats_mode, hipStream_t stream);
 
-#ifdef NESLE_STEP_FULL_TU
+#if NESLE_STEP_PART == 1
 hipError_t launch_step_full(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
                             hipStream_t stream) {
     const Geometry g = geometry(s.n, 4);   // the all-in-LDS kernel is built for 4 waves
     if (!g.full || g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
     return launch_layout<true>(s, g, frameskip, max_instr, stats_mode, stream);
 }
+#elif NESLE_STEP_PART == 2
+hipError_t launch_step_narrow(const DeviceState& s, std::uint32_t waves, std::uint32_t frameskip,
+                              std::uint32_t max_instr, int stats_mode, hipStream_t stream) {
+    const Geometry g = geometry(s.n, waves);
+    if (g.full || g.lane_bits > kNarrowLaneBits || g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
+    return launch_layout<false>(s, g, frameskip, max_instr, stats_mode, stream);
+}
 #else
 hipError_t launch_step(const DeviceState& s, std::uint32_t frameskip, std::uint32_t max_instr, int stats_mode,
                        hipStream_t stream) {
-    const Geometry g = geometry(s.n, waves_per_group());
+    const std::uint32_t waves = waves_per_group();
+    const Geometry g = geometry(s.n, waves);
     if (g.full) return launch_step_full(s, frameskip, max_instr, stats_mode, stream);
     if (g.lds > kLdsLimit) return hipErrorInvalidConfiguration;
+    if (g.lane_bits <= kNarrowLaneBits) return launch_step_narrow(s, waves, frameskip, max_instr, stats_mode, stream);
     return launch_layout<false>(s, g, frameskip, max_instr, stats_mode, stream);
 }
 #endif

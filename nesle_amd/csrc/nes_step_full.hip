@@ -3,8 +3,7 @@
 // from nes_step.hip in a translation unit of their own so that they take a
 // scheduler flag of their own (nesle_amd/build.py).  With LLVM's iterative
 // ILP scheduler these instances run 2-3 % faster (4,096 consoles: 14.22 ->
-// 13.85 ms per launch, 8,192: 14.61 -> 14.31); the split-layout instances,
-// built by nes_step.hip with the default scheduler, run 2.5 % slower with it
-// at 65,536 consoles.
-#define NESLE_STEP_FULL_TU 1
+// 13.85 ms per launch, 8,192: 14.61 -> 14.31); the split-layout instances
+// at 64 consoles per wave run 2.5 % slower with it (65,536 consoles).
+#define NESLE_STEP_PART 1
 #include "nes_step.hip"

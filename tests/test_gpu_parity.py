@@ -110,10 +110,11 @@ def test_full_size_sampled_envs(num_envs, steps):
     assert (b.host(abi.VIEW_BUDGET_HITS) == 0).all()
 
 
-@pytest.mark.parametrize("num_envs", [1, 100, 12345, 50001])
+@pytest.mark.parametrize("num_envs", [1, 100, 12345, 30001, 50001])
 def test_ragged_batch_sizes_sampled(num_envs):
     """Batch sizes that fill no whole wave or workgroup: 1 and 100 consoles
-    (all RAM in LDS), 12,345 (16 consoles a wave) and 50,001 (64 a wave, the
+    (all RAM in LDS), 12,345 and 30,001 (16 and 32 consoles a wave, the
+    split-layout kernel built for narrow waves) and 50,001 (64 a wave, the
     last wave holding 17).  Sampled consoles, the last one always among them,
     equal the oracle over 3 steps (instruction counts and rewards every step,
     state at the end)."""

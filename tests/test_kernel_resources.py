@@ -44,13 +44,13 @@ def test_render_kernel_lds_fits_five_workgroups(tmp_path):
     assert render[0]["private_segment_fixed_size"] == 0
 
 
-@pytest.mark.parametrize("source,full", [("nes_step.hip", 0), ("nes_step_full.hip", 1)])
+@pytest.mark.parametrize("source,full", [("nes_step.hip", 0), ("nes_step_full.hip", 1), ("nes_step_narrow.hip", 0)])
 def test_step_kernels_use_no_scratch(tmp_path, source, full):
     """Every step kernel but the census build (stats mode 3, a measurement
     variant whose counters may spill) keeps its state in registers and LDS.
-    The split-layout instances come from nes_step.hip, the all-RAM-in-LDS
-    ones from nes_step_full.hip (its own scheduler flag), each built with the
-    flags the package build gives it."""
+    The split-layout instances come from nes_step.hip (64 consoles per wave)
+    and nes_step_narrow.hip (16 or 32), the all-RAM-in-LDS ones from
+    nes_step_full.hip, each built with the flags the package build gives it."""
     kernels = _kernels(build.CSRC / source, tmp_path)
     steps = {k: v for k, v in kernels.items() if "step_kernel" in k and "step_kernelILi3E" not in k}
     assert len(steps) == 4
