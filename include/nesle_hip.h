@@ -47,8 +47,8 @@ enum {
     NESLE_VIEW_DONES = 2,        /* uint8  [num_envs]                       */
     NESLE_VIEW_ACTIONS = 3,      /* uint8  [num_envs]                       */
     NESLE_VIEW_INSTRUCTIONS = 4, /* uint64 [num_envs] (after stats steps)   */
-    NESLE_VIEW_FRAMES = 5,       /* uint32 [num_envs] frames completed      */
-    NESLE_VIEW_BUDGET_HITS = 6,  /* uint32 [num_envs]                       */
+    NESLE_VIEW_FRAMES = 5,       /* uint32 [num_envs] frames completed (after stats steps) */
+    NESLE_VIEW_BUDGET_HITS = 6,  /* uint32 [num_envs]   (after stats steps) */
     NESLE_VIEW_OPCODES = 7,      /* uint64 [256]     (after profile steps)  */
     NESLE_VIEW_PCS = 8,          /* uint64 [65536]                          */
     NESLE_VIEW_OAM = 9,          /* uint8  [num_envs][256] (host copy only) */

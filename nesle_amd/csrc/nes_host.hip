@@ -320,8 +320,14 @@ struct nesle_batch {
         if (stats_arena != nullptr) return;
         const std::size_t n = cfg.num_envs;
         const std::size_t a = align_up(8 * n, 256), b = align_up(4 * n, 256), c = align_up(4 * n, 256);
-        hip_check(hipMalloc(&stats_arena, a + b + c + 8 * 256 + 8 * 65536 + 8 * nesle::census::kCount),
-                  "hipMalloc stats");
+        const std::size_t total = a + b + c + 8 * 256 + 8 * 65536 + 8 * nesle::census::kCount;
+        hip_check(hipMalloc(&stats_arena, total), "hipMalloc stats");
+        // Counters read before the first statistics step read zero, not what
+        // an earlier allocation left there (a kernel, not a memset, in case
+        // the first request comes inside a stream capture).
+        hip_check(nesle::launch_zero_u64(static_cast<unsigned long long*>(stats_arena),
+                                         static_cast<std::uint32_t>(total / 8), stream),
+                  "zero stats");
         auto* base = static_cast<std::uint8_t*>(stats_arena);
         ds.stat_instructions = reinterpret_cast<std::uint64_t*>(base);
         ds.stat_frames = reinterpret_cast<std::uint32_t*>(base + a);

@@ -137,6 +137,46 @@ def test_ragged_batch_sizes_sampled(num_envs):
     assert (b.host(abi.VIEW_FRAMES) == 4).all()
 
 
+def test_kernel_builds_agree_across_batch_sizes():
+    """The production step kernel (no statistics, no frame budget) comes from
+    three builds with different scheduler flags: all RAM in LDS (up to 8,192
+    consoles), the split layout at 16 or 32 consoles per wave (16,384 and
+    32,768) and at 64 (65,536).  The first 8,192 consoles of each batch, given
+    the same pads, end every one of 4 steps with identical rewards and done
+    flags, and the last with identical RAM (all 8,192) and canonical state (a
+    sample).  The statistics counters, which only statistics steps write,
+    read zero after these steps."""
+    rom = _rom(13)
+    sizes = (8192, 16384, 32768, 65536)
+    n0 = sizes[0]
+    masks = [masks_for(777, sizes[-1], k) for k in range(4)]
+    sample = [0, 1, 63, 64, 4095, n0 - 1]
+    ref = None
+    for n in sizes:
+        say(f"[gpu] kernel builds agree: N={n} fs=4 steps=4")
+        b = abi.Batch(rom, n, frameskip=4, reward_kind=abi.REWARD_XDELTA, x_lo=synthrom.X_LO, x_hi=synthrom.X_HI,
+                      done_addr=synthrom.DONE_BYTE, clip=15, time_penalty=0.25)
+        per_step = []
+        for k in range(4):
+            b.set_actions(masks[k][:n])
+            b.step()
+            per_step.append((b.host(abi.VIEW_REWARDS)[:n0].copy(), b.host(abi.VIEW_DONES)[:n0].copy()))
+        # Steps without statistics leave the per-console counters as created: zero.
+        assert not b.host(abi.VIEW_FRAMES).any() and not b.host(abi.VIEW_INSTRUCTIONS).any()
+        got = (per_step, b.host(abi.VIEW_RAM)[:n0].copy(), [b.save_state(e) for e in sample])
+        del b
+        if ref is None:
+            assert len({row.tobytes() for row in got[1][:256]}) > 1   # the pads made the consoles diverge
+            ref = got
+            continue
+        for k, ((r0, d0), (r1, d1)) in enumerate(zip(ref[0], got[0])):
+            np.testing.assert_array_equal(r1, r0, err_msg=f"N={n} step {k} rewards")
+            np.testing.assert_array_equal(d1, d0, err_msg=f"N={n} step {k} dones")
+        np.testing.assert_array_equal(got[1], ref[1], err_msg=f"N={n} RAM")
+        for e, a, c in zip(sample, ref[2], got[2]):
+            assert np.array_equal(c, a), f"N={n} env {e}: {first_diff(c, a)}"
+
+
 def test_snapshot_autoreset_xdelta_reward():
     """Config 3 in miniature: 8 snapshots captured after seeded warm-up frames,
     done byte patched so episodes end within the run, x-delta reward with time
