@@ -46,10 +46,14 @@ HIP_FLAGS = [
 # fastest for it: all RAM in LDS (nes_step_full.hip, up to 8,192 consoles)
 # LLVM's iterative ILP scheduler, 2-3 % faster; the split layout at 16 or 32
 # consoles per wave (nes_step_narrow.hip) the machine scheduler off, 2-3 %
-# faster; at 64 per wave (nes_step.hip, 65,536 consoles) the default, as both
-# of the others run 0.6-2.5 % slower there.
+# faster; at 64 per wave (nes_step.hip, 65,536 consoles) the default strategy,
+# as both of the others run 0.6-2.5 % slower there.  Where the machine
+# scheduler runs, its macro-op fusion (keeping fusible instruction pairs
+# adjacent) is off: 2.3 % faster at 65,536 consoles, 1 % with all RAM in LDS.
+_NO_FUSION = ["-mllvm", "-misched-fusion=false"]
 SOURCE_FLAGS = {
-    CSRC / "nes_step_full.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    CSRC / "nes_step.hip": _NO_FUSION,
+    CSRC / "nes_step_full.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp", *_NO_FUSION],
     CSRC / "nes_step_narrow.hip": ["-mllvm", "-enable-misched=false"],
 }
 
